@@ -1,0 +1,258 @@
+#!/usr/bin/env python3
+"""Benchmark of the phobos leaf kernels on one MI355X.
+
+A "step" is one pass of the phobos-bench suite at the BASELINE configs:
+saxpy_fp32 (n = 4096^2), gemm_fp32, gemm_fp16tc_fp32acc and gemm_fp16
+(4096^3), flash_fp32 and flash_fp16 (B4 x H16 x 4096 x 4096 x D64), each
+launched once through libphobos_hip on one stream, inputs resident in HBM.
+
+Every launch is bracketed by HIP events on that stream, so each kernel's
+average launch time is measured live.  `value` is the headline metric's first
+figure: gemm_fp16tc_fp32acc TFLOP/s (FLOP formula 2MNK + MN, main.rs:591); the
+other kernels' figures are reported under "kernels".  saxpy rotates over four
+input sets (512 MiB) so that it streams from HBM, not the 256 MB MALL.
+
+Prints one JSON line on stdout; progress goes to stderr.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "phobos-lang_amd"))
+
+# MI355X published peaks (dense): HBM3E 8 TB/s; fp16 MFMA 2516.6 TFLOP/s;
+# fp32 matrix 157.3 TFLOP/s.
+PEAK_HBM_GBS = 8000.0
+PEAK_FP16_TFLOPS = 2516.6
+PEAK_FP32_TFLOPS = 157.3
+
+GEMM_FLOP = 2 * 4096 ** 3 + 4096 ** 2          # main.rs:591
+FLASH_FLOP = 4 * 4096 * 4096 * 64 * 64         # main.rs:1032, x 64 heads
+SAXPY_BYTES = 12 * 4096 * 4096                 # read x, read y, write y
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--kernels", default="all",
+                    help="comma list of saxpy_fp32,gemm_fp32,gemm_fp16tc_fp32acc,gemm_fp16,"
+                         "flash_fp32,flash_fp16")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    return ap.parse_args()
+
+
+class Kernel:
+    def __init__(self, name, launch, work, unit, bound, peak):
+        self.name, self.launch, self.work, self.unit = name, launch, work, unit
+        self.bound, self.peak = bound, peak
+        self.times = []
+
+
+def setup(px, stream, wanted):
+    """Allocates and fills the BASELINE-config inputs on the device."""
+    ks = []
+    N = 4096
+    if "saxpy_fp32" in wanted:
+        n = N * N
+        sets = []
+        for r in range(4):
+            x = px.DeviceBuffer.from_array(px.lcg_f32(1 + 10 * r, n))
+            y = px.DeviceBuffer.from_array(px.lcg_f32(2 + 10 * r, n))
+            sets.append((x, y))
+        state = {"i": 0}
+
+        def saxpy():
+            x, y = sets[state["i"] % 4]
+            state["i"] += 1
+            px.launch_saxpy(stream, x.ptr, y.ptr, y.ptr, n, 2.5)
+        ks.append(Kernel("saxpy_fp32", saxpy, SAXPY_BYTES / 1e9, "GB/s", "hbm", PEAK_HBM_GBS))
+        ks[-1].keep = sets
+    if "gemm_fp32" in wanted:
+        a = px.DeviceBuffer.from_array(px.lcg_f32(1, N * N))
+        b = px.DeviceBuffer.from_array(px.lcg_f32(2, N * N))
+        c = px.DeviceBuffer.from_array(px.lcg_f32(3, N * N))
+
+        def g32():
+            px.launch_gemm(stream, px.GEMM_FP32, a.ptr, b.ptr, c.ptr, N, N, N, 0.125, 1.5)
+        ks.append(Kernel("gemm_fp32", g32, GEMM_FLOP / 1e12, "TFLOP/s", "mfma", PEAK_FP32_TFLOPS))
+        ks[-1].keep = (a, b, c)
+    if "gemm_fp16tc_fp32acc" in wanted or "gemm_fp16" in wanted:
+        a32 = px.from_f16_bits(px.to_f16_bits(px.normal_f32(1, N * N, 1 / 64.0)))
+        b32 = px.from_f16_bits(px.to_f16_bits(px.normal_f32(2, N * N, 1 / 64.0)))
+    if "gemm_fp16tc_fp32acc" in wanted:
+        a = px.DeviceBuffer.from_array(a32)
+        b = px.DeviceBuffer.from_array(b32)
+        c = px.DeviceBuffer(N * N * 4)
+        c.zero(stream)
+
+        def gtc():
+            px.launch_gemm(stream, px.GEMM_FP16TC_FP32ACC, a.ptr, b.ptr, c.ptr, N, N, N, 1.0, 0.0)
+        ks.append(Kernel("gemm_fp16tc_fp32acc", gtc, GEMM_FLOP / 1e12, "TFLOP/s", "mfma",
+                         PEAK_FP16_TFLOPS))
+        ks[-1].keep = (a, b, c)
+    if "gemm_fp16" in wanted:
+        a = px.DeviceBuffer.from_array(px.to_f16_bits(a32))
+        b = px.DeviceBuffer.from_array(px.to_f16_bits(b32))
+        c = px.DeviceBuffer(N * N * 2)
+        c.zero(stream)
+
+        def g16():
+            px.launch_gemm(stream, px.GEMM_FP16, a.ptr, b.ptr, c.ptr, N, N, N, 1.0, 0.0)
+        ks.append(Kernel("gemm_fp16", g16, GEMM_FLOP / 1e12, "TFLOP/s", "mfma", PEAK_FP16_TFLOPS))
+        ks[-1].keep = (a, b, c)
+    BH, S, D = 64, 4096, 64
+    for name, kid, peak in (("flash_fp32", px.FLASH_FP32_BH, PEAK_FP32_TFLOPS),
+                            ("flash_fp16", px.FLASH_FP16_BH, PEAK_FP16_TFLOPS)):
+        if name not in wanted:
+            continue
+        ts = [px.normal_f32(s, BH * S * D) for s in (1, 2, 3)]
+        if name == "flash_fp16":
+            ts = [px.to_f16_bits(t) for t in ts]
+        q, k, v = (px.DeviceBuffer.from_array(t) for t in ts)
+        o = px.DeviceBuffer(ts[0].nbytes)
+
+        def fl(q=q, k=k, v=v, o=o, kid=kid):
+            px.launch_flash_bh(stream, kid, q.ptr, k.ptr, v.ptr, o.ptr, BH, S, S, D, 0.125)
+        ks.append(Kernel(name, fl, FLASH_FLOP / 1e12, "TFLOP/s", "mfma", peak))
+        ks[-1].keep = (q, k, v, o)
+    px.synchronize()
+    return ks
+
+
+def cpu_baseline(seconds):
+    """The oracle's f32 blocked GEMM (OpenMP) on the host cores: a bounded
+    sample of the gemm workload, 2048^3 repeated for ~`seconds`."""
+    import oracle
+    M = 2048
+    A = oracle.lcg_f32(1, M * M).reshape(M, M)
+    B = oracle.lcg_f32(2, M * M).reshape(M, M)
+    C = np.zeros((M, M), np.float32)
+    flop = 2 * M ** 3 + M * M
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        oracle.sgemm_f32(1.0, A, B, 0.0, C)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or reps >= 50:
+            break
+    return {"value": round(flop * reps / el / 1e12, 4), "unit": "TFLOP/s",
+            "cores": oracle.num_threads(), "kind": "port",
+            "sample": f"oracle orc_sgemm_f32 (f32, blocked, OpenMP), {M}^3 x {reps} reps "
+                      f"in {el:.1f} s"}
+
+
+def load_traffic():
+    p = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(p):
+        with open(p) as f:
+            return json.load(f)
+    return {}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              "(this backend has no multi-GPU path)", file=sys.stderr)
+        sys.exit(2)
+    import phobos_amd as px
+    px.init(0)
+    info = px.device_info()
+    log(f"device: {info}")
+    all_names = ["saxpy_fp32", "gemm_fp32", "gemm_fp16tc_fp32acc", "gemm_fp16", "flash_fp32",
+                 "flash_fp16"]
+    wanted = all_names if args.kernels == "all" else args.kernels.split(",")
+    stream = px.Stream()
+    ks = setup(px, stream, wanted)
+    ev = [px.Event() for _ in range(len(ks) + 1)]
+    # per-step events: ev[i] before kernel i, ev[-1] after the last
+    for _ in range(args.warmup):
+        for k in ks:
+            k.launch()
+    stream.synchronize()
+    px.synchronize()
+    step_events = []
+    t0 = time.perf_counter()
+    for s in range(args.steps):
+        evs = [px.Event() for _ in range(len(ks) + 1)]
+        for i, k in enumerate(ks):
+            evs[i].record(stream)
+            k.launch()
+        evs[-1].record(stream)
+        step_events.append(evs)
+    stream.synchronize()
+    px.synchronize()
+    wall = time.perf_counter() - t0
+    for evs in step_events:
+        for i, k in enumerate(ks):
+            k.times.append(evs[i].elapsed_ms(evs[i + 1]))
+    gpu_ms = sum(evs[0].elapsed_ms(evs[-1]) for evs in step_events)
+    for evs in step_events:
+        for e in evs:
+            e.destroy()
+
+    traffic = load_traffic()
+    kern = {}
+    for k in ks:
+        t = np.array(k.times)
+        avg = float(t.mean())
+        val = k.work / (avg / 1e3)
+        kern[k.name] = {
+            "value": round(val, 2), "unit": k.unit, "ms_avg": round(avg, 4),
+            "ms_min": round(float(t.min()), 4), "ms_median": round(float(np.median(t)), 4),
+            "roofline": {"bound": k.bound, "achieved": round(val, 2), "peak": k.peak,
+                         "unit": "GB/s" if k.bound == "hbm" else "TFLOP/s",
+                         "frac": round(val / k.peak, 4),
+                         "traffic": traffic.get(k.name)},
+        }
+        log(f"{k.name:22s} avg {avg:8.4f} ms  min {t.min():8.4f} ms  "
+            f"{val:10.2f} {k.unit}  ({100 * val / k.peak:5.1f}% of peak)")
+
+    head = "gemm_fp16tc_fp32acc"
+    hk = kern.get(head) or next(iter(kern.values()))
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline ...")
+        cpu = cpu_baseline(args.cpu_seconds)
+        log(f"cpu baseline: {cpu}")
+    out = {
+        "metric": "achieved TFLOPS & % peak: gemm_fp16tc 4096^3, flash_fp16; saxpy HBM GB/s",
+        "value": hk["value"],
+        "unit": hk["unit"],
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(gpu_ms / args.steps, 4),
+        "wall_ms_per_step": round(wall * 1e3 / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 (f32 accumulate)",
+        "data": "synthetic (Lcg / Box-Muller seeded inputs of the BASELINE shapes)",
+        "config": {"workload": "gemm_fp16tc_fp32acc M=N=K=4096, A,B=f16(N(0,1)/64) in f32 "
+                               "storage, C=0, alpha=1, beta=0; step = phobos-bench suite "
+                               "(saxpy 2^24, gemm_fp32/fp16tc/fp16 4096^3, flash fp32/fp16 "
+                               "B4xH16x4096x4096xD64)",
+                   "global_batch": 1, "seq_len": 4096, "parallelism": "none (1 GPU)"},
+        "roofline": hk["roofline"],
+        "cpu_baseline": cpu,
+        "kernels": kern,
+        "device": info,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,223 @@
+/*
+ * phobos_hip.h -- C ABI of the MI355X (gfx950) leaf-kernel backend.
+ *
+ * Everything is plain C: device addresses are uint64_t (the reference's
+ * CUdeviceptr), streams and events are opaque handles, sizes are integers.
+ * Every function returns 0 on success or a nonzero status (a HIP error code
+ * where one exists, else PHX_E_*); phx_last_error() returns the message for
+ * the calling thread.  No function here allocates device memory except the
+ * ones named *_malloc / *_create.
+ *
+ * The entry points replace, one for one, what the reference's host code does
+ * through the cust CUDA driver API:
+ *   - phobos-bench launches:  launch!(func<<<grid, block, 0, stream>>>(...))
+ *       phobos-bench/src/main.rs:290-327 (gemm), 334-371 (flash),
+ *       1227-1239 (saxpy)
+ *   - phobos-pod COMPUTE:     Engine::launch, phobos-pod/src/engine.rs:542-653
+ *   - module cache:           PtxCache, phobos-pod/src/ptx_cache.rs:12-82
+ *   - device arena:           DeviceArena / TileStore,
+ *                             phobos-pod/src/tile_store.rs:14-222
+ *   - streams / events:       engine.rs:86, 172-174, 632-687
+ */
+#ifndef PHOBOS_HIP_H
+#define PHOBOS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------ status codes */
+#define PHX_OK 0
+#define PHX_E_INVALID 1001     /* bad argument / shape the kernel does not take */
+#define PHX_E_NOT_INIT 1002    /* phx_init not called */
+#define PHX_E_NOT_FOUND 1003   /* code object or entry point missing */
+#define PHX_E_EXHAUSTED 1004   /* arena exhausted (tile_store.rs:57-63) */
+#define PHX_E_IO 1005          /* file:// storage error */
+#define PHX_E_SEGMENT 1006     /* malformed segment / instruction */
+
+/* ------------------------------------------------------------ kernel ids */
+/* The leaf kernels of the reference examples (.ph files), one code object each; the entry name
+ * inside is the .ph kernel name (main.rs:512, 761, 985, 1113, 1225;
+ * clustergen.rs:1285, 1353). */
+typedef enum {
+    PHX_SAXPY_FP32 = 0,          /* saxpy_fp32.ph            entry "saxpy", i32 idx */
+    PHX_GEMM_FP32 = 1,           /* gemm_fp32.ph             entry "gemm",  i32 idx */
+    PHX_GEMM_FP16TC_FP32ACC = 2, /* gemm_fp16tc_fp32acc.ph   entry "gemm",  i64 idx */
+    PHX_GEMM_FP16 = 3,           /* gemm_fp16.ph             entry "gemm",  i64 idx */
+    PHX_FLASH_FP32 = 4,          /* flash_attention_fp32.ph  entry "flash_attention", i64 */
+    PHX_FLASH_FP16 = 5,          /* flash_attention_fp16.ph  entry "flash_attention", i64 */
+    PHX_MATMUL = 6,              /* matmul_cluster_fp32.ph step leaf "matmul", i32 */
+    PHX_MATMUL_INIT = 7,         /* matmul_cluster_fp32.ph init leaf "matmul_init", i32 */
+    PHX_FLASH_FP32_BH = 8,       /* "flash_attention_bh": [B*H, N, D] in one launch */
+    PHX_FLASH_FP16_BH = 9,
+    PHX_NUM_KERNELS = 10
+} phx_kernel;
+
+typedef void *phx_stream;   /* a hipStream_t; NULL = the legacy default stream */
+typedef void *phx_event;    /* a hipEvent_t */
+typedef void *phx_module;   /* a hipModule_t */
+typedef void *phx_function; /* a hipFunction_t */
+typedef struct phx_arena_s *phx_arena;
+
+/* ------------------------------------------------------------ device */
+/* cust::quick_init (main.rs:169).  Loads the built-in code objects from
+ * code_object_dir (NULL: the directory holding this library, or
+ * $PHX_CODE_OBJECT_DIR). */
+int phx_init(int device, const char *code_object_dir);
+int phx_shutdown(void);
+const char *phx_last_error(void);
+/* name: >=64 bytes.  cus, clock_khz, l2/lds bytes as reported by HIP. */
+int phx_device_info(char *name, size_t name_len, int *cus, int *clock_khz, size_t *hbm_bytes,
+                    int *lds_bytes_per_cu);
+int phx_device_synchronize(void);
+
+/* ------------------------------------------------------------ memory */
+int phx_malloc(uint64_t *dptr, size_t bytes);
+int phx_free(uint64_t dptr);
+int phx_host_alloc(void **ptr, size_t bytes); /* pinned (hipHostMalloc) */
+int phx_host_free(void *ptr);
+int phx_memcpy_h2d(uint64_t dst, const void *src, size_t bytes);
+int phx_memcpy_d2h(void *dst, uint64_t src, size_t bytes);
+int phx_memcpy_d2d(uint64_t dst, uint64_t src, size_t bytes);
+int phx_memcpy_h2d_async(uint64_t dst, const void *src, size_t bytes, phx_stream s);
+int phx_memcpy_d2h_async(void *dst, uint64_t src, size_t bytes, phx_stream s);
+/* cuMemsetD8Async (main.rs:268-282) */
+int phx_memset_async(uint64_t dst, int value, size_t bytes, phx_stream s);
+
+/* ------------------------------------------------------------ streams/events */
+int phx_stream_create(phx_stream *s); /* non-blocking, default priority */
+int phx_stream_destroy(phx_stream s);
+int phx_stream_synchronize(phx_stream s);
+int phx_event_create(phx_event *e);
+int phx_event_destroy(phx_event e);
+int phx_event_record(phx_event e, phx_stream s);
+/* 0 = complete, 1 = not ready, else error (engine.rs:655-687) */
+int phx_event_query(phx_event e);
+int phx_event_synchronize(phx_event e);
+int phx_event_elapsed_ms(float *ms, phx_event start, phx_event stop);
+
+/* ------------------------------------------------------------ modules */
+/* PtxCache::insert / function (ptx_cache.rs:41-81) for gfx950 code objects. */
+int phx_module_load_data(phx_module *m, const void *image, size_t bytes);
+int phx_module_load_file(phx_module *m, const char *path);
+int phx_module_unload(phx_module m);
+int phx_module_get_function(phx_function *f, phx_module m, const char *name);
+/* The built-in code object's entry for a kernel id. */
+int phx_builtin_function(phx_function *f, phx_kernel k);
+/* Index width (32 or 64) and block size the built-in kernel expects. */
+int phx_kernel_abi(phx_kernel k, int *index_bits, uint32_t block[3]);
+
+/* ------------------------------------------------------------ launch */
+/* cuLaunchKernel semantics: one pointer per kernel parameter in args
+ * (stream.launch, engine.rs:643-647; launch!, main.rs:308-323). */
+int phx_launch(phx_function f, const uint32_t grid[3], const uint32_t block[3],
+               uint32_t shared_bytes, phx_stream s, void **args);
+
+/* Grid and block a built-in kernel wants for the given problem.
+ * dims: saxpy {n}; gemm/matmul {M, N, K}; matmul_init {M, N};
+ * flash {Nq, Nk, D}; flash_bh {BH, Nq, Nk, D}.
+ * Replaces the reference's config-derived grid (main.rs:500-508, 974-981,
+ * 1220-1223; phobos-sched/src/lib.rs:380-429). */
+int phx_grid_for(phx_kernel k, const int64_t *dims, int ndims, uint32_t grid[3],
+                 uint32_t block[3]);
+/* Validates that a built-in kernel accepts these dims (divisibility etc). */
+int phx_check_shape(phx_kernel k, const int64_t *dims, int ndims);
+
+/* --- Pod COMPUTE marshalling (engine.rs:582-630) ---
+ * Each tile argument becomes the exploded memref
+ *   (ptr, ptr, offset=0, sizes[rank], strides[rank] row-major)
+ * at the kernel's index width; scalars are placed at their parameter
+ * position `pos` as little-endian bit patterns (tile.rs:75-84: an f32 uses
+ * the low 4 bytes of `bits`).  grid/cta are passed through unchanged. */
+typedef struct {
+    uint64_t addr;
+    uint32_t rank; /* 1..3 */
+    uint64_t shape[3];
+} phx_tile_arg;
+
+typedef struct {
+    uint32_t pos;   /* parameter position among tiles+scalars */
+    uint32_t bytes; /* 4 (f32/i32) or 8 (f64/i64) */
+    uint64_t bits;
+} phx_scalar_arg;
+
+int phx_compute(phx_function f, int index_bits, const phx_tile_arg *tiles, uint32_t ntiles,
+                const phx_scalar_arg *scalars, uint32_t nscalars, const uint32_t grid[3],
+                const uint32_t cta[3], phx_stream s);
+
+/* ------------------------------------------------------------ typed launches */
+/* Each marshals the reference's exploded-memref argument list for the named
+ * .ph kernel and launches its gfx950 code object on stream s. */
+
+/* saxpy_fp32.ph: out = alpha*x + y; out may alias y (main.rs:1227-1239). */
+int phx_saxpy(phx_stream s, uint64_t x, uint64_t y, uint64_t out, int64_t n, float alpha);
+
+/* gemm (kernel = PHX_GEMM_FP32 | PHX_GEMM_FP16TC_FP32ACC | PHX_GEMM_FP16 |
+ * PHX_MATMUL): C = alpha*A@B + beta*C, row-major A[M,K] B[K,N] C[M,N]
+ * (launch_gemm, main.rs:290-327).  Element types follow the .ph signature:
+ * f32 for FP32/FP16TC/MATMUL, f16 for FP16.  PHX_MATMUL is the cluster step
+ * leaf C = alpha*A@B + C (beta is accepted and ignored, clustergen.rs:1363-1399). */
+int phx_gemm(phx_stream s, phx_kernel k, uint64_t a, uint64_t b, uint64_t c, int64_t M,
+             int64_t N, int64_t K, float alpha, float beta);
+
+/* matmul_init leaf: C = beta*C over a [M, N] f32 tile (clustergen.rs:1292-1360). */
+int phx_matmul_init(phx_stream s, uint64_t c, int64_t M, int64_t N, float beta);
+
+/* flash_attention (kernel = PHX_FLASH_FP32 | PHX_FLASH_FP16): one head,
+ * Q[Nq,D] K[Nk,D] V[Nk,D] O[Nq,D] (launch_flash, main.rs:334-371). */
+int phx_flash_attention(phx_stream s, phx_kernel k, uint64_t q, uint64_t kk, uint64_t v,
+                        uint64_t o, int64_t Nq, int64_t Nk, int64_t D, float scale);
+
+/* flash_attention_bh: BH independent heads laid out [BH, N, D] (head stride
+ * N*D), one launch.  No reference counterpart: the .ph signature is one
+ * head; per head it is the same arithmetic as flash_attention. */
+int phx_flash_attention_bh(phx_stream s, phx_kernel k, uint64_t q, uint64_t kk, uint64_t v,
+                           uint64_t o, int64_t BH, int64_t Nq, int64_t Nk, int64_t D,
+                           float scale);
+
+/* ------------------------------------------------------------ arena */
+/* DeviceArena (tile_store.rs:14-83): one device allocation, bump pointer,
+ * exact size-class free lists, 256-byte alignment, 256-byte minimum class. */
+size_t phx_size_class(size_t bytes);
+int phx_arena_create(phx_arena *a, size_t bytes);
+int phx_arena_destroy(phx_arena a);
+int phx_arena_alloc(phx_arena a, size_t bytes, uint64_t *addr, size_t *cls);
+int phx_arena_free(phx_arena a, uint64_t addr, size_t cls);
+int phx_arena_can_alloc(phx_arena a, size_t bytes); /* 1 yes, 0 no */
+int phx_arena_stats(phx_arena a, size_t *cap, size_t *bump, uint64_t *base);
+
+/* ------------------------------------------------------------ inputs */
+/* Lcg::unit_f32s (phobos-base/src/rng.rs:9-25) into host memory. */
+int phx_lcg_fill_f32(uint64_t seed, size_t n, float *out);
+/* Seeded N(0,1)*scale by Box-Muller over Lcg draws (this backend's input
+ * convention for the BASELINE configs; the reference has no normal draw). */
+int phx_normal_fill_f32(uint64_t seed, size_t n, double scale, float *out);
+/* f32 -> f16 bit patterns, IEEE round-to-nearest-even (main.rs:682-693). */
+int phx_f32_to_f16(size_t n, const float *in, uint16_t *out);
+int phx_f16_to_f32(size_t n, const uint16_t *in, float *out);
+
+/* ------------------------------------------------------------ pod segment */
+/* One-pod executor for ALLOC/LOAD/COMPUTE/STORE/FREE segments
+ * (Engine, phobos-pod/src/engine.rs:121-232, 355-398, 424-509).  The segment
+ * is given in the text form documented in INTEGRATION.md; kernels are the
+ * built-in ids.  LOAD/STORE use file:// f32 tensors (storage.rs:22-79) staged
+ * through pinned host buffers with async copies. */
+typedef struct phx_pod_s *phx_pod;
+int phx_pod_create(phx_pod *p, size_t arena_bytes, int nstreams);
+int phx_pod_destroy(phx_pod p);
+/* Registers a tensor id -> (uri, shape) for LOAD/STORE (JobManifest). */
+int phx_pod_set_tensor(phx_pod p, uint32_t tensor, const char *uri, const uint64_t *shape,
+                       uint32_t rank);
+/* Binds a segment kernel id to a built-in kernel (SetKernels). */
+int phx_pod_set_kernel(phx_pod p, uint32_t kernel_id, phx_kernel k);
+/* Runs one segment to completion.  stats (nullable) receives
+ * {n_alloc, n_load, n_compute, n_store, n_free, compute_ns, wall_ns, io_ns}. */
+int phx_pod_run_segment(phx_pod p, const char *segment_text, uint64_t stats[8]);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PHOBOS_HIP_H */

@@ -1,0 +1,37 @@
+// Launch geometry shared by the gfx950 kernels and the host runtime.
+//
+// The reference derives each grid from the autotuned .ph tile sizes
+// (phobos-bench/src/main.rs:500-508, 974-981, 1220-1223).  These kernels pick
+// their own MI355X tiles, so the host asks phx_grid_for() instead; every
+// kernel also walks its work items with a block-stride loop, so any grid the
+// caller passes still computes the whole result.
+#pragma once
+
+// saxpy: 256 threads, each handling PHX_SAXPY_VEC float4 per block step.
+#define PHX_SAXPY_THREADS 256
+#define PHX_SAXPY_VEC 4
+#define PHX_SAXPY_BLOCK_ELEMS (PHX_SAXPY_THREADS * PHX_SAXPY_VEC * 4)
+
+// f16-operand GEMMs (gemm_fp16, gemm_fp16tc_fp32acc): 256x256 output tile,
+// K step 64, 256 threads = 4 waves in a 2x2 arrangement of 128x128.
+#define PHX_H_BM 256
+#define PHX_H_BN 256
+#define PHX_H_BK 64
+#define PHX_H_THREADS 256
+
+// f32 GEMM (gemm_fp32, cluster matmul): 128x128 output tile, K step 32,
+// 256 threads = 4 waves of 64x64.
+#define PHX_S_BM 128
+#define PHX_S_BN 128
+#define PHX_S_BK 32
+#define PHX_S_THREADS 256
+
+// matmul_init: element-wise, 256 threads x 4 float4.
+#define PHX_EW_THREADS 256
+#define PHX_EW_BLOCK_ELEMS (256 * 16)
+
+// flash attention: 128 query rows per block (4 waves x 32), 64 keys per step.
+#define PHX_FA_BR 128
+#define PHX_FA_BC 64
+#define PHX_FA_THREADS 256
+#define PHX_FA_D 64

@@ -1,0 +1,637 @@
+// Host runtime of the MI355X leaf-kernel backend: the C ABI declared in
+// include/phobos_hip.h.  Everything goes through the HIP module API
+// (hipModuleLoad / hipModuleGetFunction / hipModuleLaunchKernel), the same
+// path the reference takes through cust (Module::from_ptx + launch!), so the
+// typed helpers below exercise exactly what a phobos-pod COMPUTE would.
+#include "phx_internal.h"
+
+#include <dlfcn.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <deque>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+namespace phx {
+
+static thread_local std::string g_err;
+
+int set_error(int code, const char *fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int hip_error(hipError_t e, const char *what) {
+    return set_error((int)e, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+struct KernelSpec {
+    const char *file;
+    const char *entry;
+    int index_bits;
+    uint32_t block;
+};
+
+// One code object per .ph source, as the reference compiles one module per
+// kernel file; the entry name is the .ph kernel name.
+static const KernelSpec kSpecs[PHX_NUM_KERNELS] = {
+    {"saxpy_fp32.hsaco", "saxpy", 32, PHX_SAXPY_THREADS},
+    {"gemm_fp32.hsaco", "gemm", 32, PHX_S_THREADS},
+    {"gemm_fp16tc_fp32acc.hsaco", "gemm", 64, PHX_H_THREADS},
+    {"gemm_fp16.hsaco", "gemm", 64, PHX_H_THREADS},
+    {"flash_attention_fp32.hsaco", "flash_attention", 64, PHX_FA_THREADS},
+    {"flash_attention_fp16.hsaco", "flash_attention", 64, PHX_FA_THREADS},
+    {"matmul_cluster_fp32.hsaco", "matmul", 32, PHX_S_THREADS},
+    {"matmul_cluster_fp32.hsaco", "matmul_init", 32, PHX_EW_THREADS},
+    {"flash_attention_fp32.hsaco", "flash_attention_bh", 64, PHX_FA_THREADS},
+    {"flash_attention_fp16.hsaco", "flash_attention_bh", 64, PHX_FA_THREADS},
+};
+
+struct State {
+    bool init = false;
+    int device = -1;
+    std::string dir;
+    std::unordered_map<std::string, hipModule_t> modules;  // file -> module
+    hipFunction_t fns[PHX_NUM_KERNELS] = {};
+    std::mutex mu;
+};
+static State g;
+
+static std::string default_dir() {
+    if (const char *env = getenv("PHX_CODE_OBJECT_DIR")) return env;
+    Dl_info info;
+    if (dladdr((void *)&default_dir, &info) && info.dli_fname) {
+        std::string p = info.dli_fname;
+        size_t slash = p.rfind('/');
+        if (slash != std::string::npos) return p.substr(0, slash);
+    }
+    return ".";
+}
+
+static int ensure_init() {
+    if (!g.init) return set_error(PHX_E_NOT_INIT, "phx_init has not been called");
+    return PHX_OK;
+}
+
+int builtin(phx_kernel k, hipFunction_t *out) {
+    if (int rc = ensure_init()) return rc;
+    if ((int)k < 0 || k >= PHX_NUM_KERNELS)
+        return set_error(PHX_E_INVALID, "unknown kernel id %d", (int)k);
+    std::lock_guard<std::mutex> lock(g.mu);
+    if (!g.fns[k]) {
+        const KernelSpec &s = kSpecs[k];
+        hipModule_t mod;
+        auto it = g.modules.find(s.file);
+        if (it == g.modules.end()) {
+            std::string path = g.dir + "/" + s.file;
+            hipError_t e = hipModuleLoad(&mod, path.c_str());
+            if (e != hipSuccess)
+                return set_error(PHX_E_NOT_FOUND,
+                                 "cannot load code object %s: %s (build the backend first)",
+                                 path.c_str(), hipGetErrorString(e));
+            g.modules[s.file] = mod;
+        } else {
+            mod = it->second;
+        }
+        hipFunction_t f;
+        hipError_t e = hipModuleGetFunction(&f, mod, s.entry);
+        if (e != hipSuccess)
+            return set_error(PHX_E_NOT_FOUND, "entry '%s' not in %s: %s", s.entry, s.file,
+                             hipGetErrorString(e));
+        g.fns[k] = f;
+    }
+    *out = g.fns[k];
+    return PHX_OK;
+}
+
+// ------------------------------------------------------------------ args
+// Holds the values of an exploded-memref argument list at stable addresses
+// plus the void* array hipModuleLaunchKernel reads.
+struct ArgPack {
+    std::deque<uint64_t> slots;  // deque: push_back keeps earlier addresses valid
+    std::vector<void *> ptrs;
+    explicit ArgPack(size_t cap) { ptrs.reserve(cap); }
+    void push_bits(uint64_t v) {
+        slots.push_back(v);
+        ptrs.push_back(&slots.back());
+    }
+    void ptr(uint64_t p) { push_bits(p); }
+    void idx(int64_t v, int bits) {
+        if (bits == 32) {
+            int32_t v32 = (int32_t)v;
+            uint32_t u;
+            memcpy(&u, &v32, 4);
+            push_bits((uint64_t)u);  // little-endian: low 4 bytes hold the i32
+        } else {
+            uint64_t u;
+            memcpy(&u, &v, 8);
+            push_bits(u);
+        }
+    }
+    void f32(float f) {
+        uint32_t u;
+        memcpy(&u, &f, 4);
+        push_bits((uint64_t)u);
+    }
+    // (ptr, ptr, 0, sizes..., row-major strides...)
+    void memref(uint64_t p, const int64_t *shape, int rank, int bits) {
+        ptr(p);
+        ptr(p);
+        idx(0, bits);
+        for (int i = 0; i < rank; ++i) idx(shape[i], bits);
+        int64_t stride = 1;
+        int64_t strides[4];
+        for (int i = rank - 1; i >= 0; --i) {
+            strides[i] = stride;
+            stride *= shape[i];
+        }
+        for (int i = 0; i < rank; ++i) idx(strides[i], bits);
+    }
+};
+
+int launch_raw(hipFunction_t f, const uint32_t grid[3], const uint32_t block[3], uint32_t shmem,
+               hipStream_t s, void **args) {
+    hipError_t e = hipModuleLaunchKernel(f, grid[0], grid[1], grid[2], block[0], block[1],
+                                         block[2], shmem, s, args, nullptr);
+    if (e != hipSuccess) return hip_error(e, "hipModuleLaunchKernel");
+    return PHX_OK;
+}
+
+static bool fits_i32(int64_t v) { return v >= 0 && v <= INT32_MAX; }
+
+int check_shape(phx_kernel k, const int64_t *d, int nd) {
+    auto need = [&](int n) {
+        if (nd != n)
+            return set_error(PHX_E_INVALID, "kernel %d takes %d dims, got %d", (int)k, n, nd);
+        for (int i = 0; i < n; ++i)
+            if (d[i] < 0) return set_error(PHX_E_INVALID, "negative dimension %lld", (long long)d[i]);
+        return PHX_OK;
+    };
+    switch (k) {
+    case PHX_SAXPY_FP32:
+        if (int rc = need(1)) return rc;
+        if (!fits_i32(d[0])) return set_error(PHX_E_INVALID, "saxpy n=%lld exceeds i32 index", (long long)d[0]);
+        return PHX_OK;
+    case PHX_GEMM_FP16TC_FP32ACC:
+    case PHX_GEMM_FP16:
+        if (int rc = need(3)) return rc;
+        if (d[0] == 0 || d[1] == 0 || d[2] == 0 || d[0] % PHX_H_BM || d[1] % PHX_H_BN ||
+            d[2] % PHX_H_BK)
+            return set_error(PHX_E_INVALID,
+                             "f16 gemm needs M%%%d==0, N%%%d==0, K%%%d==0 (got %lld,%lld,%lld)",
+                             PHX_H_BM, PHX_H_BN, PHX_H_BK, (long long)d[0], (long long)d[1],
+                             (long long)d[2]);
+        return PHX_OK;
+    case PHX_GEMM_FP32:
+    case PHX_MATMUL:
+        if (int rc = need(3)) return rc;
+        if (d[0] == 0 || d[1] == 0 || d[2] == 0 || d[0] % PHX_S_BM || d[1] % PHX_S_BN ||
+            d[2] % PHX_S_BK)
+            return set_error(PHX_E_INVALID,
+                             "f32 gemm needs M%%%d==0, N%%%d==0, K%%%d==0 (got %lld,%lld,%lld)",
+                             PHX_S_BM, PHX_S_BN, PHX_S_BK, (long long)d[0], (long long)d[1],
+                             (long long)d[2]);
+        if (!fits_i32(d[0] * d[2]) || !fits_i32(d[2] * d[1]) || !fits_i32(d[0] * d[1]))
+            return set_error(PHX_E_INVALID, "f32 gemm extents exceed the i32 index");
+        return PHX_OK;
+    case PHX_MATMUL_INIT:
+        if (int rc = need(2)) return rc;
+        if (!fits_i32(d[0] * d[1])) return set_error(PHX_E_INVALID, "matmul_init exceeds i32 index");
+        return PHX_OK;
+    case PHX_FLASH_FP32:
+    case PHX_FLASH_FP16:
+        if (int rc = need(3)) return rc;
+        if (d[2] != PHX_FA_D || d[0] == 0 || d[1] == 0 || d[0] % PHX_FA_BR || d[1] % PHX_FA_BC)
+            return set_error(PHX_E_INVALID,
+                             "flash needs D==%d, Nq%%%d==0, Nk%%%d==0 (got Nq=%lld Nk=%lld D=%lld)",
+                             PHX_FA_D, PHX_FA_BR, PHX_FA_BC, (long long)d[0], (long long)d[1],
+                             (long long)d[2]);
+        return PHX_OK;
+    case PHX_FLASH_FP32_BH:
+    case PHX_FLASH_FP16_BH:
+        if (int rc = need(4)) return rc;
+        if (d[0] == 0 || d[0] > 65535)
+            return set_error(PHX_E_INVALID, "flash_bh needs 1 <= BH <= 65535");
+        return check_shape(k == PHX_FLASH_FP32_BH ? PHX_FLASH_FP32 : PHX_FLASH_FP16, d + 1, 3);
+    default:
+        return set_error(PHX_E_INVALID, "unknown kernel id %d", (int)k);
+    }
+}
+
+int grid_for(phx_kernel k, const int64_t *d, int nd, uint32_t grid[3], uint32_t block[3]) {
+    if ((int)k < 0 || k >= PHX_NUM_KERNELS)
+        return set_error(PHX_E_INVALID, "unknown kernel id %d", (int)k);
+    if (int rc = check_shape(k, d, nd)) return rc;
+    grid[0] = grid[1] = grid[2] = 1;
+    block[0] = kSpecs[k].block;
+    block[1] = block[2] = 1;
+    switch (k) {
+    case PHX_SAXPY_FP32: {
+        int64_t b = (d[0] + PHX_SAXPY_BLOCK_ELEMS - 1) / PHX_SAXPY_BLOCK_ELEMS;
+        grid[0] = (uint32_t)(b < 1 ? 1 : b);
+        break;
+    }
+    case PHX_GEMM_FP16TC_FP32ACC:
+    case PHX_GEMM_FP16:
+        grid[0] = (uint32_t)((d[0] / PHX_H_BM) * (d[1] / PHX_H_BN));
+        break;
+    case PHX_GEMM_FP32:
+    case PHX_MATMUL:
+        grid[0] = (uint32_t)((d[0] / PHX_S_BM) * (d[1] / PHX_S_BN));
+        break;
+    case PHX_MATMUL_INIT: {
+        int64_t n = d[0] * d[1];
+        int64_t b = (n + PHX_EW_BLOCK_ELEMS - 1) / PHX_EW_BLOCK_ELEMS;
+        grid[0] = (uint32_t)(b < 1 ? 1 : b);
+        break;
+    }
+    case PHX_FLASH_FP32:
+    case PHX_FLASH_FP16:
+        grid[0] = (uint32_t)(d[0] / PHX_FA_BR);
+        break;
+    case PHX_FLASH_FP32_BH:
+    case PHX_FLASH_FP16_BH:
+        grid[0] = (uint32_t)(d[1] / PHX_FA_BR);
+        grid[1] = (uint32_t)d[0];
+        break;
+    default:
+        break;
+    }
+    return PHX_OK;
+}
+
+int kernel_abi(phx_kernel k, int *bits, uint32_t block[3]) {
+    if ((int)k < 0 || k >= PHX_NUM_KERNELS)
+        return set_error(PHX_E_INVALID, "unknown kernel id %d", (int)k);
+    if (bits) *bits = kSpecs[k].index_bits;
+    if (block) {
+        block[0] = kSpecs[k].block;
+        block[1] = block[2] = 1;
+    }
+    return PHX_OK;
+}
+
+}  // namespace phx
+
+using namespace phx;
+
+extern "C" {
+
+const char *phx_last_error(void) { return g_err.c_str(); }
+
+int phx_init(int device, const char *dir) {
+    hipError_t e = hipSetDevice(device);
+    if (e != hipSuccess) return hip_error(e, "hipSetDevice");
+    e = hipFree(nullptr);  // force context creation
+    if (e != hipSuccess) return hip_error(e, "hipFree(0)");
+    std::lock_guard<std::mutex> lock(g.mu);
+    if (g.init && g.device != device)
+        return set_error(PHX_E_INVALID, "already initialised on device %d", g.device);
+    g.device = device;
+    g.dir = dir ? std::string(dir) : default_dir();
+    g.init = true;
+    return PHX_OK;
+}
+
+int phx_shutdown(void) {
+    std::lock_guard<std::mutex> lock(g.mu);
+    for (auto &kv : g.modules) (void)hipModuleUnload(kv.second);
+    g.modules.clear();
+    for (auto &f : g.fns) f = nullptr;
+    g.init = false;
+    return PHX_OK;
+}
+
+int phx_device_info(char *name, size_t name_len, int *cus, int *clock_khz, size_t *hbm,
+                    int *lds) {
+    if (int rc = ensure_init()) return rc;
+    hipDeviceProp_t p;
+    hipError_t e = hipGetDeviceProperties(&p, g.device);
+    if (e != hipSuccess) return hip_error(e, "hipGetDeviceProperties");
+    if (name && name_len) {
+        snprintf(name, name_len, "%s (%s)", p.name, p.gcnArchName);
+    }
+    if (cus) *cus = p.multiProcessorCount;
+    if (clock_khz) *clock_khz = p.clockRate;
+    if (hbm) *hbm = p.totalGlobalMem;
+    if (lds) *lds = (int)p.maxSharedMemoryPerMultiProcessor;
+    return PHX_OK;
+}
+
+int phx_device_synchronize(void) {
+    hipError_t e = hipDeviceSynchronize();
+    return e == hipSuccess ? PHX_OK : hip_error(e, "hipDeviceSynchronize");
+}
+
+// ------------------------------------------------------------------ memory
+int phx_malloc(uint64_t *dptr, size_t bytes) {
+    void *p = nullptr;
+    hipError_t e = hipMalloc(&p, bytes ? bytes : 1);
+    if (e != hipSuccess) return hip_error(e, "hipMalloc");
+    *dptr = (uint64_t)(uintptr_t)p;
+    return PHX_OK;
+}
+int phx_free(uint64_t dptr) {
+    hipError_t e = hipFree((void *)(uintptr_t)dptr);
+    return e == hipSuccess ? PHX_OK : hip_error(e, "hipFree");
+}
+int phx_host_alloc(void **ptr, size_t bytes) {
+    hipError_t e = hipHostMalloc(ptr, bytes ? bytes : 1, hipHostMallocDefault);
+    return e == hipSuccess ? PHX_OK : hip_error(e, "hipHostMalloc");
+}
+int phx_host_free(void *ptr) {
+    hipError_t e = hipHostFree(ptr);
+    return e == hipSuccess ? PHX_OK : hip_error(e, "hipHostFree");
+}
+int phx_memcpy_h2d(uint64_t dst, const void *src, size_t bytes) {
+    hipError_t e = hipMemcpy((void *)(uintptr_t)dst, src, bytes, hipMemcpyHostToDevice);
+    return e == hipSuccess ? PHX_OK : hip_error(e, "hipMemcpy H2D");
+}
+int phx_memcpy_d2h(void *dst, uint64_t src, size_t bytes) {
+    hipError_t e = hipMemcpy(dst, (const void *)(uintptr_t)src, bytes, hipMemcpyDeviceToHost);
+    return e == hipSuccess ? PHX_OK : hip_error(e, "hipMemcpy D2H");
+}
+int phx_memcpy_d2d(uint64_t dst, uint64_t src, size_t bytes) {
+    hipError_t e = hipMemcpy((void *)(uintptr_t)dst, (const void *)(uintptr_t)src, bytes,
+                             hipMemcpyDeviceToDevice);
+    return e == hipSuccess ? PHX_OK : hip_error(e, "hipMemcpy D2D");
+}
+int phx_memcpy_h2d_async(uint64_t dst, const void *src, size_t bytes, phx_stream s) {
+    hipError_t e = hipMemcpyAsync((void *)(uintptr_t)dst, src, bytes, hipMemcpyHostToDevice,
+                                  (hipStream_t)s);
+    return e == hipSuccess ? PHX_OK : hip_error(e, "hipMemcpyAsync H2D");
+}
+int phx_memcpy_d2h_async(void *dst, uint64_t src, size_t bytes, phx_stream s) {
+    hipError_t e = hipMemcpyAsync(dst, (const void *)(uintptr_t)src, bytes,
+                                  hipMemcpyDeviceToHost, (hipStream_t)s);
+    return e == hipSuccess ? PHX_OK : hip_error(e, "hipMemcpyAsync D2H");
+}
+int phx_memset_async(uint64_t dst, int value, size_t bytes, phx_stream s) {
+    hipError_t e = hipMemsetAsync((void *)(uintptr_t)dst, value, bytes, (hipStream_t)s);
+    return e == hipSuccess ? PHX_OK : hip_error(e, "hipMemsetAsync");
+}
+
+// ------------------------------------------------------------------ streams/events
+int phx_stream_create(phx_stream *s) {
+    hipStream_t h;
+    hipError_t e = hipStreamCreateWithFlags(&h, hipStreamNonBlocking);
+    if (e != hipSuccess) return hip_error(e, "hipStreamCreateWithFlags");
+    *s = (phx_stream)h;
+    return PHX_OK;
+}
+int phx_stream_destroy(phx_stream s) {
+    hipError_t e = hipStreamDestroy((hipStream_t)s);
+    return e == hipSuccess ? PHX_OK : hip_error(e, "hipStreamDestroy");
+}
+int phx_stream_synchronize(phx_stream s) {
+    hipError_t e = hipStreamSynchronize((hipStream_t)s);
+    return e == hipSuccess ? PHX_OK : hip_error(e, "hipStreamSynchronize");
+}
+int phx_event_create(phx_event *ev) {
+    hipEvent_t h;
+    hipError_t e = hipEventCreate(&h);
+    if (e != hipSuccess) return hip_error(e, "hipEventCreate");
+    *ev = (phx_event)h;
+    return PHX_OK;
+}
+int phx_event_destroy(phx_event ev) {
+    hipError_t e = hipEventDestroy((hipEvent_t)ev);
+    return e == hipSuccess ? PHX_OK : hip_error(e, "hipEventDestroy");
+}
+int phx_event_record(phx_event ev, phx_stream s) {
+    hipError_t e = hipEventRecord((hipEvent_t)ev, (hipStream_t)s);
+    return e == hipSuccess ? PHX_OK : hip_error(e, "hipEventRecord");
+}
+int phx_event_query(phx_event ev) {
+    hipError_t e = hipEventQuery((hipEvent_t)ev);
+    if (e == hipSuccess) return 0;
+    if (e == hipErrorNotReady) return 1;
+    return hip_error(e, "hipEventQuery");
+}
+int phx_event_synchronize(phx_event ev) {
+    hipError_t e = hipEventSynchronize((hipEvent_t)ev);
+    return e == hipSuccess ? PHX_OK : hip_error(e, "hipEventSynchronize");
+}
+int phx_event_elapsed_ms(float *ms, phx_event a, phx_event b) {
+    hipError_t e = hipEventElapsedTime(ms, (hipEvent_t)a, (hipEvent_t)b);
+    return e == hipSuccess ? PHX_OK : hip_error(e, "hipEventElapsedTime");
+}
+
+// ------------------------------------------------------------------ modules
+int phx_module_load_data(phx_module *m, const void *image, size_t bytes) {
+    if (int rc = ensure_init()) return rc;
+    if (!image || !bytes) return set_error(PHX_E_INVALID, "empty code object image");
+    hipModule_t h;
+    hipError_t e = hipModuleLoadData(&h, image);
+    if (e != hipSuccess) return hip_error(e, "hipModuleLoadData");
+    *m = (phx_module)h;
+    return PHX_OK;
+}
+int phx_module_load_file(phx_module *m, const char *path) {
+    if (int rc = ensure_init()) return rc;
+    hipModule_t h;
+    hipError_t e = hipModuleLoad(&h, path);
+    if (e != hipSuccess) return hip_error(e, "hipModuleLoad");
+    *m = (phx_module)h;
+    return PHX_OK;
+}
+int phx_module_unload(phx_module m) {
+    hipError_t e = hipModuleUnload((hipModule_t)m);
+    return e == hipSuccess ? PHX_OK : hip_error(e, "hipModuleUnload");
+}
+int phx_module_get_function(phx_function *f, phx_module m, const char *name) {
+    hipFunction_t h;
+    hipError_t e = hipModuleGetFunction(&h, (hipModule_t)m, name);
+    if (e != hipSuccess) return set_error(PHX_E_NOT_FOUND, "entry '%s': %s", name, hipGetErrorString(e));
+    *f = (phx_function)h;
+    return PHX_OK;
+}
+int phx_builtin_function(phx_function *f, phx_kernel k) {
+    hipFunction_t h;
+    if (int rc = builtin(k, &h)) return rc;
+    *f = (phx_function)h;
+    return PHX_OK;
+}
+int phx_kernel_abi(phx_kernel k, int *index_bits, uint32_t block[3]) {
+    return kernel_abi(k, index_bits, block);
+}
+
+// ------------------------------------------------------------------ launch
+int phx_launch(phx_function f, const uint32_t grid[3], const uint32_t block[3],
+               uint32_t shared_bytes, phx_stream s, void **args) {
+    if (!f) return set_error(PHX_E_INVALID, "null function");
+    return launch_raw((hipFunction_t)f, grid, block, shared_bytes, (hipStream_t)s, args);
+}
+
+int phx_grid_for(phx_kernel k, const int64_t *dims, int ndims, uint32_t grid[3],
+                 uint32_t block[3]) {
+    return grid_for(k, dims, ndims, grid, block);
+}
+int phx_check_shape(phx_kernel k, const int64_t *dims, int ndims) {
+    return check_shape(k, dims, ndims);
+}
+
+int phx_compute(phx_function f, int bits, const phx_tile_arg *tiles, uint32_t ntiles,
+                const phx_scalar_arg *scalars, uint32_t nscalars, const uint32_t grid[3],
+                const uint32_t cta[3], phx_stream s) {
+    if (!f) return set_error(PHX_E_INVALID, "null function");
+    if (bits != 32 && bits != 64) return set_error(PHX_E_INVALID, "index_bits must be 32 or 64");
+    ArgPack pack((size_t)ntiles * 9 + nscalars + 1);
+    uint32_t total = ntiles + nscalars;
+    uint32_t next_tile = 0;
+    for (uint32_t pos = 0; pos < total; ++pos) {
+        const phx_scalar_arg *sc = nullptr;
+        for (uint32_t i = 0; i < nscalars; ++i)
+            if (scalars[i].pos == pos) sc = &scalars[i];
+        if (sc) {
+            if (sc->bytes != 4 && sc->bytes != 8)
+                return set_error(PHX_E_INVALID, "scalar at %u has %u bytes", pos, sc->bytes);
+            pack.push_bits(sc->bytes == 4 ? (sc->bits & 0xffffffffu) : sc->bits);
+            continue;
+        }
+        if (next_tile >= ntiles)
+            return set_error(PHX_E_INVALID, "parameter %u: no tile left and no scalar at it", pos);
+        const phx_tile_arg &t = tiles[next_tile++];
+        if (t.rank < 1 || t.rank > 3) return set_error(PHX_E_INVALID, "tile rank %u", t.rank);
+        int64_t shape[3];
+        for (uint32_t i = 0; i < t.rank; ++i) {
+            shape[i] = (int64_t)t.shape[i];
+            if (bits == 32 && !fits_i32(shape[i]))
+                return set_error(PHX_E_INVALID, "tile dim %lld exceeds the i32 index", (long long)shape[i]);
+        }
+        pack.memref(t.addr, shape, (int)t.rank, bits);
+    }
+    if (next_tile != ntiles) return set_error(PHX_E_INVALID, "%u tiles left unplaced", ntiles - next_tile);
+    return launch_raw((hipFunction_t)f, grid, cta, 0, (hipStream_t)s, pack.ptrs.data());
+}
+
+// ------------------------------------------------------------------ typed launches
+static int launch_builtin(phx_kernel k, const int64_t *dims, int nd, ArgPack &pack,
+                          hipStream_t s) {
+    hipFunction_t f;
+    if (int rc = builtin(k, &f)) return rc;
+    uint32_t grid[3], block[3];
+    if (int rc = grid_for(k, dims, nd, grid, block)) return rc;
+    return launch_raw(f, grid, block, 0, s, pack.ptrs.data());
+}
+
+int phx_saxpy(phx_stream s, uint64_t x, uint64_t y, uint64_t out, int64_t n, float alpha) {
+    int64_t d[1] = {n};
+    ArgPack p(20);
+    p.memref(x, d, 1, 32);
+    p.memref(y, d, 1, 32);
+    p.memref(out, d, 1, 32);
+    p.f32(alpha);
+    return launch_builtin(PHX_SAXPY_FP32, d, 1, p, (hipStream_t)s);
+}
+
+int phx_gemm(phx_stream s, phx_kernel k, uint64_t a, uint64_t b, uint64_t c, int64_t M,
+             int64_t N, int64_t K, float alpha, float beta) {
+    if (k != PHX_GEMM_FP32 && k != PHX_GEMM_FP16TC_FP32ACC && k != PHX_GEMM_FP16 &&
+        k != PHX_MATMUL)
+        return set_error(PHX_E_INVALID, "kernel %d is not a gemm", (int)k);
+    int bits = kSpecs[k].index_bits;
+    int64_t d[3] = {M, N, K};
+    int64_t sa[2] = {M, K}, sb[2] = {K, N}, sc[2] = {M, N};
+    ArgPack p(24);
+    p.memref(a, sa, 2, bits);
+    p.memref(b, sb, 2, bits);
+    p.memref(c, sc, 2, bits);
+    p.f32(alpha);
+    p.f32(beta);
+    return launch_builtin(k, d, 3, p, (hipStream_t)s);
+}
+
+int phx_matmul_init(phx_stream s, uint64_t c, int64_t M, int64_t N, float beta) {
+    int64_t d[2] = {M, N};
+    ArgPack p(10);
+    p.memref(c, d, 2, 32);
+    p.f32(beta);
+    return launch_builtin(PHX_MATMUL_INIT, d, 2, p, (hipStream_t)s);
+}
+
+int phx_flash_attention(phx_stream s, phx_kernel k, uint64_t q, uint64_t kk, uint64_t v,
+                        uint64_t o, int64_t Nq, int64_t Nk, int64_t D, float scale) {
+    if (k != PHX_FLASH_FP32 && k != PHX_FLASH_FP16)
+        return set_error(PHX_E_INVALID, "kernel %d is not a single-head flash", (int)k);
+    int64_t d[3] = {Nq, Nk, D};
+    int64_t sq[2] = {Nq, D}, sk[2] = {Nk, D};
+    ArgPack p(32);
+    p.memref(q, sq, 2, 64);
+    p.memref(kk, sk, 2, 64);
+    p.memref(v, sk, 2, 64);
+    p.memref(o, sq, 2, 64);
+    p.f32(scale);
+    return launch_builtin(k, d, 3, p, (hipStream_t)s);
+}
+
+int phx_flash_attention_bh(phx_stream s, phx_kernel k, uint64_t q, uint64_t kk, uint64_t v,
+                           uint64_t o, int64_t BH, int64_t Nq, int64_t Nk, int64_t D,
+                           float scale) {
+    if (k != PHX_FLASH_FP32_BH && k != PHX_FLASH_FP16_BH)
+        return set_error(PHX_E_INVALID, "kernel %d is not a batched flash", (int)k);
+    int64_t d[4] = {BH, Nq, Nk, D};
+    int64_t sq[3] = {BH, Nq, D}, sk[3] = {BH, Nk, D};
+    ArgPack p(44);
+    p.memref(q, sq, 3, 64);
+    p.memref(kk, sk, 3, 64);
+    p.memref(v, sk, 3, 64);
+    p.memref(o, sq, 3, 64);
+    p.f32(scale);
+    return launch_builtin(k, d, 4, p, (hipStream_t)s);
+}
+
+// ------------------------------------------------------------------ inputs
+int phx_lcg_fill_f32(uint64_t seed, size_t n, float *out) {
+    uint64_t st = seed;
+    for (size_t i = 0; i < n; ++i) {
+        st = st * 6364136223846793005ULL + 1442695040888963407ULL;
+        out[i] = (float)(st >> 33) / 2147483648.0f - 1.0f;
+    }
+    return PHX_OK;
+}
+
+int phx_normal_fill_f32(uint64_t seed, size_t n, double scale, float *out) {
+    uint64_t st = seed;
+    const double two_pi = 6.283185307179586476925286766559;
+    for (size_t i = 0; i < n; i += 2) {
+        st = st * 6364136223846793005ULL + 1442695040888963407ULL;
+        uint64_t a = st;
+        st = st * 6364136223846793005ULL + 1442695040888963407ULL;
+        uint64_t b = st;
+        double u1 = (double)((a >> 11) + 1) * 0x1.0p-53;
+        double u2 = (double)(b >> 11) * 0x1.0p-53;
+        double r = std::sqrt(-2.0 * std::log(u1));
+        out[i] = (float)(r * std::cos(two_pi * u2) * scale);
+        if (i + 1 < n) out[i + 1] = (float)(r * std::sin(two_pi * u2) * scale);
+    }
+    return PHX_OK;
+}
+
+int phx_f32_to_f16(size_t n, const float *in, uint16_t *out) {
+    for (size_t i = 0; i < n; ++i) {
+        _Float16 h = (_Float16)in[i];  // IEEE RNE
+        memcpy(&out[i], &h, 2);
+    }
+    return PHX_OK;
+}
+int phx_f16_to_f32(size_t n, const uint16_t *in, float *out) {
+    for (size_t i = 0; i < n; ++i) {
+        _Float16 h;
+        memcpy(&h, &in[i], 2);
+        out[i] = (float)h;
+    }
+    return PHX_OK;
+}
+
+}  // extern "C"

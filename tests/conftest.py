@@ -12,3 +12,16 @@ for p in (ROOT, os.path.join(ROOT, "phobos-lang_amd")):
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
     config.addinivalue_line("markers", "slow: long-running CPU test")
+
+
+@pytest.fixture(scope="session")
+def px_gpu():
+    """Initialises the HIP backend on device 0 (fails loudly without a GPU)."""
+    import phobos_amd as px
+    px.init(0)
+    return px
+
+
+@pytest.fixture(scope="session")
+def stream(px_gpu):
+    return px_gpu.Stream()

