@@ -60,73 +60,86 @@ class Kernel:
         self.times = []
 
 
+def _need(buf, nbytes, what):
+    """Host-side check that a device buffer holds what the kernel will touch."""
+    if buf.nbytes < nbytes:
+        raise RuntimeError(f"{what}: buffer of {buf.nbytes} B < {nbytes} B the kernel accesses")
+
+
 def setup(px, stream, wanted):
-    """Allocates and fills the BASELINE-config inputs on the device."""
+    """Allocates and fills the BASELINE-config inputs on the device.  Every
+    launch closure binds its own buffers (no late-bound names) and the sizes
+    are checked against what the kernel reads and writes."""
     ks = []
     N = 4096
+
+    def gemm_kernel(name, kid, a, b, c, esz, alpha, beta, peak):
+        for buf, what in ((a, "A"), (b, "B"), (c, "C")):
+            _need(buf, N * N * esz, f"{name} {what}")
+
+        def launch():
+            px.launch_gemm(stream, kid, a, b, c, N, N, N, alpha, beta)
+        k = Kernel(name, launch, GEMM_FLOP / 1e12, "TFLOP/s", "mfma", peak)
+        k.keep = (a, b, c)
+        return k
+
     if "saxpy_fp32" in wanted:
         n = N * N
         sets = []
         for r in range(4):
             x = px.DeviceBuffer.from_array(px.lcg_f32(1 + 10 * r, n))
             y = px.DeviceBuffer.from_array(px.lcg_f32(2 + 10 * r, n))
+            _need(x, 4 * n, "saxpy x")
+            _need(y, 4 * n, "saxpy y")
             sets.append((x, y))
-        state = {"i": 0}
 
-        def saxpy():
+        def saxpy(sets=sets, state={"i": 0}):
             x, y = sets[state["i"] % 4]
             state["i"] += 1
-            px.launch_saxpy(stream, x.ptr, y.ptr, y.ptr, n, 2.5)
-        ks.append(Kernel("saxpy_fp32", saxpy, SAXPY_BYTES / 1e9, "GB/s", "hbm", PEAK_HBM_GBS))
-        ks[-1].keep = sets
+            px.launch_saxpy(stream, x, y, y, n, 2.5)
+        k = Kernel("saxpy_fp32", saxpy, SAXPY_BYTES / 1e9, "GB/s", "hbm", PEAK_HBM_GBS)
+        k.keep = sets
+        ks.append(k)
     if "gemm_fp32" in wanted:
-        a = px.DeviceBuffer.from_array(px.lcg_f32(1, N * N))
-        b = px.DeviceBuffer.from_array(px.lcg_f32(2, N * N))
-        c = px.DeviceBuffer.from_array(px.lcg_f32(3, N * N))
-
-        def g32():
-            px.launch_gemm(stream, px.GEMM_FP32, a.ptr, b.ptr, c.ptr, N, N, N, 0.125, 1.5)
-        ks.append(Kernel("gemm_fp32", g32, GEMM_FLOP / 1e12, "TFLOP/s", "mfma", PEAK_FP32_TFLOPS))
-        ks[-1].keep = (a, b, c)
+        ks.append(gemm_kernel("gemm_fp32", px.GEMM_FP32,
+                              px.DeviceBuffer.from_array(px.lcg_f32(1, N * N)),
+                              px.DeviceBuffer.from_array(px.lcg_f32(2, N * N)),
+                              px.DeviceBuffer.from_array(px.lcg_f32(3, N * N)),
+                              4, 0.125, 1.5, PEAK_FP32_TFLOPS))
     if "gemm_fp16tc_fp32acc" in wanted or "gemm_fp16" in wanted:
         a32 = px.from_f16_bits(px.to_f16_bits(px.normal_f32(1, N * N, 1 / 64.0)))
         b32 = px.from_f16_bits(px.to_f16_bits(px.normal_f32(2, N * N, 1 / 64.0)))
     if "gemm_fp16tc_fp32acc" in wanted:
-        a = px.DeviceBuffer.from_array(a32)
-        b = px.DeviceBuffer.from_array(b32)
         c = px.DeviceBuffer(N * N * 4)
         c.zero(stream)
-
-        def gtc():
-            px.launch_gemm(stream, px.GEMM_FP16TC_FP32ACC, a.ptr, b.ptr, c.ptr, N, N, N, 1.0, 0.0)
-        ks.append(Kernel("gemm_fp16tc_fp32acc", gtc, GEMM_FLOP / 1e12, "TFLOP/s", "mfma",
-                         PEAK_FP16_TFLOPS))
-        ks[-1].keep = (a, b, c)
+        ks.append(gemm_kernel("gemm_fp16tc_fp32acc", px.GEMM_FP16TC_FP32ACC,
+                              px.DeviceBuffer.from_array(a32), px.DeviceBuffer.from_array(b32),
+                              c, 4, 1.0, 0.0, PEAK_FP16_TFLOPS))
     if "gemm_fp16" in wanted:
-        a = px.DeviceBuffer.from_array(px.to_f16_bits(a32))
-        b = px.DeviceBuffer.from_array(px.to_f16_bits(b32))
         c = px.DeviceBuffer(N * N * 2)
         c.zero(stream)
-
-        def g16():
-            px.launch_gemm(stream, px.GEMM_FP16, a.ptr, b.ptr, c.ptr, N, N, N, 1.0, 0.0)
-        ks.append(Kernel("gemm_fp16", g16, GEMM_FLOP / 1e12, "TFLOP/s", "mfma", PEAK_FP16_TFLOPS))
-        ks[-1].keep = (a, b, c)
+        ks.append(gemm_kernel("gemm_fp16", px.GEMM_FP16,
+                              px.DeviceBuffer.from_array(px.to_f16_bits(a32)),
+                              px.DeviceBuffer.from_array(px.to_f16_bits(b32)),
+                              c, 2, 1.0, 0.0, PEAK_FP16_TFLOPS))
     BH, S, D = 64, 4096, 64
-    for name, kid, peak in (("flash_fp32", px.FLASH_FP32_BH, PEAK_FP32_TFLOPS),
-                            ("flash_fp16", px.FLASH_FP16_BH, PEAK_FP16_TFLOPS)):
+    for name, kid, peak, esz in (("flash_fp32", px.FLASH_FP32_BH, PEAK_FP32_TFLOPS, 4),
+                                 ("flash_fp16", px.FLASH_FP16_BH, PEAK_FP16_TFLOPS, 2)):
         if name not in wanted:
             continue
         ts = [px.normal_f32(s, BH * S * D) for s in (1, 2, 3)]
-        if name == "flash_fp16":
+        if esz == 2:
             ts = [px.to_f16_bits(t) for t in ts]
         q, k, v = (px.DeviceBuffer.from_array(t) for t in ts)
-        o = px.DeviceBuffer(ts[0].nbytes)
+        o = px.DeviceBuffer(BH * S * D * esz)
+        for buf, what in ((q, "Q"), (k, "K"), (v, "V"), (o, "O")):
+            _need(buf, BH * S * D * esz, f"{name} {what}")
 
         def fl(q=q, k=k, v=v, o=o, kid=kid):
-            px.launch_flash_bh(stream, kid, q.ptr, k.ptr, v.ptr, o.ptr, BH, S, S, D, 0.125)
-        ks.append(Kernel(name, fl, FLASH_FLOP / 1e12, "TFLOP/s", "mfma", peak))
-        ks[-1].keep = (q, k, v, o)
+            px.launch_flash_bh(stream, kid, q, k, v, o, BH, S, S, D, 0.125)
+        kk = Kernel(name, fl, FLASH_FLOP / 1e12, "TFLOP/s", "mfma", peak)
+        kk.keep = (q, k, v, o)
+        ks.append(kk)
     px.synchronize()
     return ks
 

@@ -220,7 +220,7 @@ class DeviceBuffer:
         return out
 
     def zero(self, stream=None):
-        check(lib().phx_memset_async(self.ptr, 0, self.nbytes, stream))
+        check(lib().phx_memset_async(self.ptr, 0, self.nbytes, _sh(stream)))
 
     def free(self):
         if self.ptr:
@@ -287,27 +287,52 @@ def _sh(stream):
 
 
 # ------------------------------------------------------------------- launches
+def _addr(buf, nbytes, what):
+    """Device address of `buf` (a DeviceBuffer or a raw address).  For a
+    DeviceBuffer the size is checked against the bytes the kernel touches, so
+    a wrong buffer raises on the host instead of faulting the GPU."""
+    if isinstance(buf, DeviceBuffer):
+        if buf.nbytes < nbytes:
+            raise PhxError(PHX_E_INVALID, f"{what}: buffer holds {buf.nbytes} B, kernel "
+                                          f"accesses {nbytes} B")
+        return buf.ptr
+    return int(buf)
+
+
+_GEMM_ESZ = {GEMM_FP32: 4, GEMM_FP16TC_FP32ACC: 4, GEMM_FP16: 2, MATMUL: 4}
+
+
 def launch_saxpy(stream, x, y, out, n, alpha):
     """saxpy_fp32.ph: out = alpha*x + y (main.rs:1227-1239)."""
-    check(lib().phx_saxpy(_sh(stream), x, y, out, n, alpha))
+    check(lib().phx_saxpy(_sh(stream), _addr(x, 4 * n, "x"), _addr(y, 4 * n, "y"),
+                          _addr(out, 4 * n, "out"), n, alpha))
 
 
 def launch_gemm(stream, kernel, a, b, c, M, N, K, alpha, beta):
     """C = alpha*A@B + beta*C for the gemm-family kernel ids (main.rs:290-327)."""
-    check(lib().phx_gemm(_sh(stream), kernel, a, b, c, M, N, K, alpha, beta))
+    e = _GEMM_ESZ.get(kernel, 4)
+    check(lib().phx_gemm(_sh(stream), kernel, _addr(a, e * M * K, "A"), _addr(b, e * K * N, "B"),
+                         _addr(c, e * M * N, "C"), M, N, K, alpha, beta))
 
 
 def launch_matmul_init(stream, c, M, N, beta):
-    check(lib().phx_matmul_init(_sh(stream), c, M, N, beta))
+    check(lib().phx_matmul_init(_sh(stream), _addr(c, 4 * M * N, "C"), M, N, beta))
 
 
 def launch_flash(stream, kernel, q, k, v, o, Nq, Nk, D, scale):
     """One-head flash attention (main.rs:334-371)."""
-    check(lib().phx_flash_attention(_sh(stream), kernel, q, k, v, o, Nq, Nk, D, scale))
+    e = 2 if kernel == FLASH_FP16 else 4
+    check(lib().phx_flash_attention(_sh(stream), kernel, _addr(q, e * Nq * D, "Q"),
+                                    _addr(k, e * Nk * D, "K"), _addr(v, e * Nk * D, "V"),
+                                    _addr(o, e * Nq * D, "O"), Nq, Nk, D, scale))
 
 
 def launch_flash_bh(stream, kernel, q, k, v, o, BH, Nq, Nk, D, scale):
-    check(lib().phx_flash_attention_bh(_sh(stream), kernel, q, k, v, o, BH, Nq, Nk, D, scale))
+    e = 2 if kernel == FLASH_FP16_BH else 4
+    check(lib().phx_flash_attention_bh(_sh(stream), kernel, _addr(q, e * BH * Nq * D, "Q"),
+                                       _addr(k, e * BH * Nk * D, "K"),
+                                       _addr(v, e * BH * Nk * D, "V"),
+                                       _addr(o, e * BH * Nq * D, "O"), BH, Nq, Nk, D, scale))
 
 
 def grid_for(kernel, dims):

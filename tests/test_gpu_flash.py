@@ -63,7 +63,8 @@ def test_flash_large_scores_and_single_block(px_gpu, stream, bits):
     D = 64
     for Nk in (64, 512):
         q = _inputs((128, D), bits, 5, 3.0)[0]
-        _, k, v = _inputs((Nk, D), bits, 7, 3.0)
+        _, k, _ = _inputs((Nk, D), bits, 7, 3.0)
+        v = _inputs((Nk, D), bits, 7, 1.0)[2]
         dq, dk, dv = (_upload(px_gpu, t, bits) for t in (q, k, v))
         do = px_gpu.DeviceBuffer(128 * D * 4)
         kern = px_gpu.FLASH_FP16 if bits == 16 else px_gpu.FLASH_FP32

@@ -48,7 +48,10 @@ def test_gemm_fp32_full_small(px_gpu, stream, M, N, K):
     C = oracle.lcg_f32(3, M * N).reshape(M, N)
     got = _gemm(px_gpu, stream, px_gpu.GEMM_FP32, A, B, C, 0.125, 1.5)
     want = oracle.gemm_full(A, B, C, 0.125, 1.5)
-    rel = np.abs(got - want) / np.maximum(np.abs(want), np.finfo(np.float64).tiny)
+    # 0.125*dot + 1.5*c can cancel at small K, so the relative error is floored
+    # at 1% of the output RMS (at 4096^3 nothing cancels and the floor is unused).
+    floor = 1e-2 * np.sqrt(np.mean(want ** 2))
+    rel = np.abs(got - want) / np.maximum(np.abs(want), floor)
     assert rel.max() < 1e-4, rel.max()
     # zero-mean operands (cancellation): RMS-normalised bound
     A2 = oracle.normal_f32(4, M * K).reshape(M, K)
