@@ -1,0 +1,88 @@
+"""The matmul_cluster config on one pod: ALLOC/LOAD/COMPUTE/STORE/FREE with
+async copies, file:// tensors, checked against the f64 oracle.
+
+Tolerance: relative error <= 1e-4 (the reference checks 1e-3,
+cluster_correctness.rs:344-375; the north star tightens it).  Lcg inputs are
+all in [-1, 0], so 0.125*A@B + 1.5*C does not cancel at these sizes."""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from phobos_amd import cluster as cl
+
+pytestmark = pytest.mark.gpu
+
+
+def test_small_job_full_check(px_gpu, tmp_path):
+    M = N = K = 1024
+    stats, paths, ins = cl.run_matmul_job(str(tmp_path), M, N, K, 256, 512, 256, 0.125, 1.5)
+    c = cl.count_ops(ins)
+    assert stats["alloc"] == c["ALLOC"] and stats["load"] == c["LOAD"]
+    assert stats["compute"] == c["COMPUTE"] and stats["store"] == c["STORE"]
+    assert stats["free"] == c["FREE"]
+    A = oracle.lcg_f32(1, M * K).reshape(M, K)
+    B = oracle.lcg_f32(2, K * N).reshape(K, N)
+    C = oracle.lcg_f32(3, M * N).reshape(M, N)
+    got = np.fromfile(paths[cl.C], np.float32).reshape(M, N)
+    want = oracle.gemm_full(A, B, C, 0.125, 1.5)
+    rel = np.abs(got - want) / np.abs(want)
+    assert rel.max() < 1e-4, rel.max()
+    # inputs are untouched
+    assert np.array_equal(np.fromfile(paths[cl.A], np.float32), A.ravel())
+
+
+def test_chain_matches_leaf_replay(px_gpu, tmp_path):
+    # init C = fl(1.5*C), then C = fl(fl(0.125*acc_k) + C) per K supertile
+    M, N, K, TM, TN, TK = 256, 256, 512, 256, 256, 128
+    stats, paths, _ = cl.run_matmul_job(str(tmp_path), M, N, K, TM, TN, TK, 0.125, 1.5)
+    A = oracle.lcg_f32(1, M * K).reshape(M, K)
+    B = oracle.lcg_f32(2, K * N).reshape(K, N)
+    want = oracle.matmul_init(1.5, oracle.lcg_f32(3, M * N).reshape(M, N))
+    for k0 in range(0, K, TK):
+        acc = oracle.gemm_full(A[:, k0:k0 + TK], B[k0:k0 + TK], None, 1.0, 0.0).astype(np.float32)
+        want = oracle.matmul_step_epilogue(0.125, acc, want)
+    got = np.fromfile(paths[cl.C], np.float32).reshape(M, N)
+    assert (np.abs(got - want) / np.abs(want)).max() < 1e-5
+
+
+def test_arena_exhausted_is_reported(px_gpu, tmp_path):
+    import phobos_amd as px
+    with pytest.raises(px.PhxError) as e:
+        cl.run_matmul_job(str(tmp_path), 512, 512, 512, 256, 256, 256, 0.125, 1.5,
+                          arena_bytes=1 << 16)
+    assert e.value.code == px.PHX_E_EXHAUSTED
+
+
+def test_malformed_segment_rejected(px_gpu):
+    import phobos_amd as px
+    pod = cl.Pod(1 << 20, 2)
+    with pytest.raises(px.PhxError) as e:
+        pod.run("1 - ALLOC 0x1 16x16 f32\n2 7 FREE 0x1 0\n")
+    assert e.value.code == 1006
+    with pytest.raises(px.PhxError):
+        pod.run("1 - BOGUS 0x1\n")
+    pod.close()
+
+
+def test_baseline_job_16384(px_gpu, tmp_path):
+    # matmul_cluster config: 16384^3 f32, supertiles 4096/8192/4096,
+    # alpha 0.125, beta 1.5, A/B/C from Lcg seeds 1/2/3 in 1 GiB files.
+    M = N = K = 16384
+    print(f"[cluster] writing inputs to {tmp_path}", flush=True)
+    stats, paths, ins = cl.run_matmul_job(str(tmp_path), M, N, K, 4096, 8192, 4096, 0.125, 1.5)
+    print(f"[cluster] stats {stats}", flush=True)
+    assert (stats["alloc"], stats["load"], stats["compute"], stats["store"], stats["free"]) == \
+        (32, 32, 40, 8, 32)
+    A = np.memmap(paths[cl.A], np.float32, "r", shape=(M, K))
+    B = np.memmap(paths[cl.B], np.float32, "r", shape=(K, N))
+    Cin = oracle.lcg_f32(3, M * N)
+    got = np.memmap(paths[cl.C], np.float32, "r", shape=(M, N))
+    r, c = oracle.sample_points(M, N, 12)
+    for i, j in zip(r.astype(int), c.astype(int)):
+        want = 0.125 * np.dot(A[i].astype(np.float64), B[:, j].astype(np.float64)) + \
+            1.5 * float(Cin[i * N + j])
+        assert abs(got[i, j] - want) / abs(want) < 1e-4, (i, j, got[i, j], want)
+    tflops = 2 * M * N * K / (stats["compute_ns"] * 1e-9) / 1e12
+    print(f"[cluster] compute {tflops:.1f} TFLOP/s, wall {stats['wall_ns'] / 1e9:.2f} s", flush=True)
