@@ -50,6 +50,9 @@ def parse():
                          "flash_fp32,flash_fp16")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run 3 device-to-device copies of 256 MiB (the plain copy the "
+                         "FETCH_SIZE/WRITE_SIZE counters are scaled by) and exit")
     return ap.parse_args()
 
 
@@ -182,6 +185,14 @@ def main():
         sys.exit(2)
     import phobos_amd as px
     px.init(0)
+    if args.copy_calibration:
+        nbytes = 256 << 20
+        src, dst = px.DeviceBuffer(nbytes), px.DeviceBuffer(nbytes)
+        for _ in range(3):
+            px.check(px.lib().phx_memcpy_d2d(dst.ptr, src.ptr, nbytes))
+        px.synchronize()
+        print(json.dumps({"copy_calibration_bytes": nbytes, "copies": 3}))
+        return
     info = px.device_info()
     log(f"device: {info}")
     all_names = ["saxpy_fp32", "gemm_fp32", "gemm_fp16tc_fp32acc", "gemm_fp16", "flash_fp32",
