@@ -55,8 +55,16 @@ typedef float T;
 #endif
 #define TILE_BYTES (BC * ROW_BYTES)  // BC == D == 64 rows
 
+// LDS serves 64 banks x 4 bytes per clock on gfx950, so a 16-lane group of a
+// 16-byte access must hit 16 distinct 16-byte slots of a 256-byte line.
+// 128-byte rows: two rows share a line, XOR the chunk with (row>>1)&7;
+// 256-byte rows: XOR with row&15.
 __device__ __forceinline__ uint32_t lds_off(uint32_t row, uint32_t chunk) {
-    return row * ROW_BYTES + ((chunk ^ (row & 7)) << 4);
+#ifdef PHX_FLASH_F16
+    return row * ROW_BYTES + ((chunk ^ ((row >> 1) & 7)) << 4);
+#else
+    return row * ROW_BYTES + ((chunk ^ (row & 15)) << 4);
+#endif
 }
 
 __device__ __forceinline__ float shfl_xor32(float v) { return __shfl_xor(v, 32, 64); }

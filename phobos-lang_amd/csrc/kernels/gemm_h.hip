@@ -25,8 +25,11 @@
 //   * K step 64.  A is staged as As[m][k], B transposed to Bs[n][k], so every
 //     MFMA operand is one ds_read_b128 (8 consecutive k of one row/column).
 //     Rows are 128 bytes; the 16-byte chunk index is XOR-swizzled with
-//     (row & 7), which makes both the staging writes and the operand reads
-//     bank-conflict free.
+//     ((row >> 1) & 7): gfx950's LDS serves 64 banks (256 bytes) per clock, so
+//     the 16 lanes of a 16-byte access must land in 16 distinct slots of a
+//     256-byte line, which makes the staging writes and operand reads
+//     conflict free (SQ_LDS_BANK_CONFLICT was a third of LDS cycles with a
+//     32-bank swizzle).
 //   * B (row-major [K,N]) is transposed in registers: each thread loads an 8x8
 //     block (8 rows of 16 bytes) and re-packs it with v_perm into 8 k-runs.
 //   * LDS double buffer (2 x 64 KiB); the next K step's global loads are in
@@ -52,13 +55,21 @@ typedef _Float16 TOut;
 #define WM 128  // wave tile rows
 #define WN 128  // wave tile cols
 #define GROUP_M 4
+// Prefetch distance in K steps: two register stages for f16 inputs (64
+// VGPRs each); the f32 inputs of the tc variant need 128 VGPRs per stage, so
+// it keeps one.
+#ifdef PHX_GEMM_TC
+#define PREFETCH 1
+#else
+#define PREFETCH 2
+#endif
 
 // LDS: [buffer][row][64 halves], 16-byte chunks swizzled by (row & 7).
 #define LDS_ROW_BYTES (BK * 2)
 #define LDS_TILE_BYTES (BM * LDS_ROW_BYTES)
 
 __device__ __forceinline__ uint32_t lds_off(uint32_t row, uint32_t chunk) {
-    return row * LDS_ROW_BYTES + ((chunk ^ (row & 7)) << 4);
+    return row * LDS_ROW_BYTES + ((chunk ^ ((row >> 1) & 7)) << 4);
 }
 
 // Global loads of one K step, held in registers until written to LDS.
@@ -72,31 +83,52 @@ struct Stage {
 #endif
 };
 
+// Buffer resource over `bytes` bytes from p (gfx9 dword3 = 0x00020000).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t phx_rsrc(const void *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes,
+                                             0x00020000);
+}
+
+template <typename V>
+__device__ __forceinline__ V buf_load(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
+}
+
+// One K step of A (BM x BK at row m0, col k0) and B (BK x BN at row k0,
+// col n0).  The buffer bases move with k0, so every per-lane offset is a
+// small 32-bit VGPR constant and the per-load offsets are scalars.
+//   A: row = i*32 + tid/8, 8 k values at chunk tid%8
+//   B: 8x8 block, rows k0 + 8*(tid%8) + i, cols n0 + 8*(tid/8) .. +7
 __device__ __forceinline__ void load_stage(Stage &st, const TIn *A, int64_t lda, const TIn *B,
                                            int64_t ldb, uint32_t m0, uint32_t n0, uint32_t k0,
-                                           uint32_t tid) {
-    // A: row = i*32 + tid/8, chunk (8 k values) = tid%8
-    const uint32_t ar = tid >> 3, ac = tid & 7;
+                                           uint32_t voa, uint32_t vob, bool valid) {
+    // A step past K (the padding step of an odd step count) gets empty
+    // buffer ranges: out-of-range buffer loads return zeros.
+    const uint32_t esz = sizeof(TIn);
+    const __amdgpu_buffer_rsrc_t ra =
+        phx_rsrc(A + (int64_t)m0 * lda + (valid ? k0 : 0),
+                 valid ? (uint32_t)((BM - 1) * lda + BK) * esz : 0u);
+    const __amdgpu_buffer_rsrc_t rb =
+        phx_rsrc(B + (int64_t)(valid ? k0 : 0) * ldb + n0,
+                 valid ? (uint32_t)((BK - 1) * ldb + BN) * esz : 0u);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const TIn *p = A + (int64_t)(m0 + i * 32 + ar) * lda + k0 + ac * 8;
+        const uint32_t so = (uint32_t)(i * 32 * lda) * esz;
 #ifdef PHX_GEMM_TC
-        st.a[i][0] = *(const phx_f4 *)p;
-        st.a[i][1] = *(const phx_f4 *)(p + 4);
+        st.a[i][0] = buf_load<phx_f4>(ra, voa, so);
+        st.a[i][1] = buf_load<phx_f4>(ra, voa + 16, so);
 #else
-        st.a[i] = *(const phx_u4 *)p;
+        st.a[i] = buf_load<phx_u4>(ra, voa, so);
 #endif
     }
-    // B: 8x8 block, k rows 8*(tid%8)+i, n cols 8*(tid/8)..+7
-    const uint32_t bk = tid & 7, bn = tid >> 3;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const TIn *p = B + (int64_t)(k0 + bk * 8 + i) * ldb + n0 + bn * 8;
+        const uint32_t so = (uint32_t)(i * ldb) * esz;
 #ifdef PHX_GEMM_TC
-        st.b[i][0] = *(const phx_f4 *)p;
-        st.b[i][1] = *(const phx_f4 *)(p + 4);
+        st.b[i][0] = buf_load<phx_f4>(rb, vob, so);
+        st.b[i][1] = buf_load<phx_f4>(rb, vob + 16, so);
 #else
-        st.b[i] = *(const phx_u4 *)p;
+        st.b[i] = buf_load<phx_u4>(rb, vob, so);
 #endif
     }
 }
@@ -166,7 +198,56 @@ __device__ __forceinline__ void store_stage(const Stage &st, char *As, char *Bs,
 #endif
 }
 
-extern "C" __global__ __launch_bounds__(NT, 1) void gemm(PHX_MEMREF2(TIn, a, int64_t),
+// One K step: compute from LDS buffer `cur`; issue the loads of step kt+2
+// into `mine` (free: its previous contents were stored at the end of step
+// kt-1); at the end store `next` (step kt+1, loaded during step kt-1) into
+// LDS buffer `nxt`.
+__device__ __forceinline__ void k_step(phx_f16v (&acc)[4][4], Stage &mine, Stage &next,
+                                       const TIn *A, int64_t lda, const TIn *B, int64_t ldb,
+                                       uint32_t m0, uint32_t n0, uint32_t kt, uint32_t nk,
+                                       uint32_t nkv, uint32_t voa, uint32_t vob, char (*cur)[LDS_TILE_BYTES],
+                                       char (*nxt)[LDS_TILE_BYTES], uint32_t wm, uint32_t wn,
+                                       uint32_t lrow, uint32_t lgrp, uint32_t tid) {
+    const char *As = cur[0];
+    const char *Bs = cur[1];
+    phx_h8 af[2][4], bf[2][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        af[0][i] = *(const phx_h8 *)(As + lds_off(wm + i * 32 + lrow, lgrp));
+        bf[0][i] = *(const phx_h8 *)(Bs + lds_off(wn + i * 32 + lrow, lgrp));
+    }
+    if (kt + PREFETCH < nk)
+        load_stage(mine, A, lda, B, ldb, m0, n0, (kt + PREFETCH) * BK, voa, vob,
+                   kt + PREFETCH < nkv);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (uint32_t s = 0; s < BK / 16; ++s) {
+        const uint32_t b = s & 1;
+        // The wave issues in order: the next slice's LDS reads go out ahead
+        // of this slice's 16 MFMAs (fenced so the scheduler keeps them
+        // there), so their latency hides under the MFMAs.
+        if (s + 1 < BK / 16) {
+            const uint32_t chunk = 2 * (s + 1) + lgrp;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                af[b ^ 1][i] = *(const phx_h8 *)(As + lds_off(wm + i * 32 + lrow, chunk));
+                bf[b ^ 1][i] = *(const phx_h8 *)(Bs + lds_off(wn + i * 32 + lrow, chunk));
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[i][j] =
+                    __builtin_amdgcn_mfma_f32_32x32x16_f16(af[b][i], bf[b][j], acc[i][j], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (kt + 1 < nk) store_stage(next, nxt[0], nxt[1], tid);
+    __syncthreads();
+}
+
+extern "C" __global__ __launch_bounds__(NT, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm(PHX_MEMREF2(TIn, a, int64_t),
                                                           PHX_MEMREF2(TIn, b, int64_t),
                                                           PHX_MEMREF2(TOut, c, int64_t),
                                                           float alpha, float beta) {
@@ -192,10 +273,16 @@ extern "C" __global__ __launch_bounds__(NT, 1) void gemm(PHX_MEMREF2(TIn, a, int
     const uint32_t tiles_n = (uint32_t)(N / BN);
     const uint32_t ntiles = (uint32_t)(M / BM) * tiles_n;
     const uint32_t nblk = phx_block_count();
-    const uint32_t nk = (uint32_t)(K / BK);
+    // K steps, padded to even: the pipeline runs in pairs of steps, and a
+    // padding step multiplies zeros.
+    const uint32_t nkv = (uint32_t)(K / BK);
+    const uint32_t nk = (nkv + 1) & ~1u;
 
     const uint32_t lrow = lane & 31;  // MFMA operand row/col within a 32 tile
     const uint32_t lgrp = lane >> 5;  // k half (0/1) inside a 16-wide k slice
+    // per-lane byte offsets of the staging loads (see load_stage)
+    const uint32_t voa = (uint32_t)(((tid >> 3) * lda + (tid & 7) * 8) * sizeof(TIn));
+    const uint32_t vob = (uint32_t)(((tid & 7) * 8 * ldb + (tid >> 3) * 8) * sizeof(TIn));
 
     for (uint32_t t = phx_block_linear(); t < ntiles; t += nblk) {
         const uint32_t ts = nblk == ntiles ? phx_xcd_swizzle(t, ntiles) : t;
@@ -215,56 +302,65 @@ extern "C" __global__ __launch_bounds__(NT, 1) void gemm(PHX_MEMREF2(TIn, a, int
             for (int j = 0; j < 4; ++j)
                 acc[i][j] = (phx_f16v){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 
-        Stage st;
-        load_stage(st, A, lda, B, ldb, m0, n0, 0, tid);
-        store_stage(st, lds[0][0], lds[0][1], tid);
+        // PREFETCH == 2: the loads of K step t+2 are issued while step t
+        // computes and written to LDS at the end of step t+1, so each load has
+        // two steps of MFMA time to land.  PREFETCH == 1: one stage, loaded
+        // during step t and stored at its end.
+        Stage st0;
+#if PREFETCH == 2
+        Stage st1;
+#else
+        Stage &st1 = st0;
+#endif
+        load_stage(st0, A, lda, B, ldb, m0, n0, 0, voa, vob, true);
+        store_stage(st0, lds[0][0], lds[0][1], tid);
+#if PREFETCH == 2
+        load_stage(st0, A, lda, B, ldb, m0, n0, BK, voa, vob, nkv > 1);
         __syncthreads();
-
-        for (uint32_t kt = 0; kt < nk; ++kt) {
-            const uint32_t cur = kt & 1;
-            if (kt + 1 < nk) load_stage(st, A, lda, B, ldb, m0, n0, (kt + 1) * BK, tid);
-            const char *As = lds[cur][0];
-            const char *Bs = lds[cur][1];
-#pragma unroll
-            for (uint32_t s = 0; s < BK / 16; ++s) {
-                const uint32_t chunk = 2 * s + lgrp;
-                phx_h8 af[4], bf[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    af[i] = *(const phx_h8 *)(As + lds_off(wm + i * 32 + lrow, chunk));
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    bf[j] = *(const phx_h8 *)(Bs + lds_off(wn + j * 32 + lrow, chunk));
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-#pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        acc[i][j] =
-                            __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-            }
-            if (kt + 1 < nk) store_stage(st, lds[cur ^ 1][0], lds[cur ^ 1][1], tid);
-            __syncthreads();
+        for (uint32_t kt = 0; kt < nk; kt += 2) {
+            k_step(acc, st1, st0, A, lda, B, ldb, m0, n0, kt, nk, nkv, voa, vob, lds[0], lds[1],
+                   wm, wn, lrow, lgrp, tid);
+            k_step(acc, st0, st1, A, lda, B, ldb, m0, n0, kt + 1, nk, nkv, voa, vob, lds[1],
+                   lds[0], wm, wn, lrow, lgrp, tid);
         }
+#else
+        __syncthreads();
+        for (uint32_t kt = 0; kt < nk; kt += 2) {
+            k_step(acc, st0, st1, A, lda, B, ldb, m0, n0, kt, nk, nkv, voa, vob, lds[0], lds[1],
+                   wm, wn, lrow, lgrp, tid);
+            k_step(acc, st0, st1, A, lda, B, ldb, m0, n0, kt + 1, nk, nkv, voa, vob, lds[1],
+                   lds[0], wm, wn, lrow, lgrp, tid);
+        }
+#endif
 
         // Epilogue.  acc[i][j][r]: row = 8*(r/4) + 4*lgrp + r%4, col = lrow.
-        const bool read_c = beta != 0.0f;
+        if (beta != 0.0f) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint32_t col = n0 + wn + j * 32 + lrow;
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t col = n0 + wn + j * 32 + lrow;
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const uint32_t row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * lgrp + (r & 3);
-                    TOut *pc = C + (int64_t)row * ldc + col;
-                    float v = alpha * acc[i][j][r];
-                    if (read_c) {
+                    for (int r = 0; r < 16; ++r) {
+                        const uint32_t row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * lgrp + (r & 3);
+                        TOut *pc = C + (int64_t)row * ldc + col;
+                        float v = alpha * acc[i][j][r];
                         float cb = beta * (float)*pc;
-                        v = v + cb;
+                        *pc = (TOut)(v + cb);
                     }
-                    *pc = (TOut)v;
                 }
-            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t col = n0 + wn + j * 32 + lrow;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const uint32_t row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * lgrp + (r & 3);
+                        C[(int64_t)row * ldc + col] = (TOut)(alpha * acc[i][j][r]);
+                    }
+                }
         }
     }
 }

@@ -24,7 +24,8 @@
 //     MFMAs read four consecutive k from one ds_read_b128: lane group g of MFMA
 //     s uses k = 8q + 4g + s.  A is staged As[m][k], B transposed to Bs[n][k]
 //     (a free 4x4 register transpose); 128-byte rows with the 16-byte chunk
-//     XOR-swizzled by (row & 7) keep writes and reads conflict free.
+//     XOR-swizzled by ((row >> 1) & 7) keep writes and reads conflict free
+//     on the 64-bank LDS.
 //   * Double-buffered LDS with the next K step's loads in flight during the
 //     current step's MFMAs; XCD-aware grouped tile order as in gemm_h.hip.
 #include "phx_common.h"
@@ -40,7 +41,7 @@
 #define LDS_TILE_BYTES (BM * LDS_ROW_BYTES)
 
 __device__ __forceinline__ uint32_t lds_off(uint32_t row, uint32_t chunk) {
-    return row * LDS_ROW_BYTES + ((chunk ^ (row & 7)) << 4);
+    return row * LDS_ROW_BYTES + ((chunk ^ ((row >> 1) & 7)) << 4);
 }
 
 struct Stage {
