@@ -54,6 +54,12 @@ typedef float T;
 #define ROW_BYTES (D * 4)  // 256 bytes
 #endif
 #define TILE_BYTES (BC * ROW_BYTES)  // BC == D == 64 rows
+// two workgroups (8 waves) per CU for the f16 path
+#ifdef PHX_FLASH_F16
+#define FA_MIN_BLOCKS 2
+#else
+#define FA_MIN_BLOCKS 1
+#endif
 
 // LDS serves 64 banks x 4 bytes per clock on gfx950, so a 16-lane group of a
 // 16-byte access must hit 16 distinct 16-byte slots of a 256-byte line.
@@ -70,31 +76,41 @@ __device__ __forceinline__ uint32_t lds_off(uint32_t row, uint32_t chunk) {
 __device__ __forceinline__ float shfl_xor32(float v) { return __shfl_xor(v, 32, 64); }
 
 #ifdef PHX_FLASH_F16
-// ---------------------------------------------------------------- f16 staging
-// Waves 0-1 stage V^T, waves 2-3 stage K; each thread issues 4 x 16-byte loads.
+// ---------------------------------------------------------------- f16 path
+// Threads 0-127 stage V^T, threads 128-255 stage K; 4 x 16-byte buffer loads
+// each.  K runs one block ahead of V: during block j the LDS holds K_{j+1}
+// (for the next scores) and V_j (for this block's P.V).
 struct Stage {
     phx_u4 r[4];
 };
 
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t phx_rsrc(const void *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes,
+                                             0x00020000);
+}
+
 // V thread v (0..127): c = v/32 (16-key group), h = (v/16)%2, b' = (v/8)%2,
 // db = v%8: rows key = 16c + 8b' + 4h + i (i<4), d = 8db..8db+7.
-// K thread u (0..127): 4 chunks, row = u/2 + 0/64?, see below.
-__device__ __forceinline__ void load_stage(Stage &st, const T *Kp, const T *Vp, int64_t ldk,
-                                           int64_t ldv, uint32_t key0, uint32_t tid) {
+// K thread u (0..127): rows i*16 + u/8 (i<4), 16-byte chunk u%8.
+// vo: this thread's byte offset inside a block (see flash_block).
+__device__ __forceinline__ void load_stage(Stage &st, __amdgpu_buffer_rsrc_t rk,
+                                           __amdgpu_buffer_rsrc_t rv, uint32_t kbytes_row,
+                                           uint32_t vbytes_row, uint32_t kblk, uint32_t vblk,
+                                           bool kval, bool vval, uint32_t vo, uint32_t tid) {
     if (tid < 128) {
-        const uint32_t v = tid;
-        const uint32_t db = v & 7, bp = (v >> 3) & 1, h = (v >> 4) & 1, c = v >> 5;
-        const uint32_t krow = 16 * c + 8 * bp + 4 * h;
+        if (vval) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                st.r[i] = __builtin_bit_cast(
+                    phx_u4, __builtin_amdgcn_raw_buffer_load_b128(
+                                rv, (int)(vo + i * vbytes_row), (int)(vblk * BC * vbytes_row), 0));
+        }
+    } else if (kval) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            st.r[i] = *(const phx_u4 *)(Vp + (int64_t)(key0 + krow + i) * ldv + 8 * db);
-    } else {
-        const uint32_t u = tid - 128;  // 128 threads x 4 chunks = 64 rows x 8 chunks
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t row = i * 16 + (u >> 3), ch = u & 7;
-            st.r[i] = *(const phx_u4 *)(Kp + (int64_t)(key0 + row) * ldk + 8 * ch);
-        }
+            st.r[i] = __builtin_bit_cast(
+                phx_u4, __builtin_amdgcn_raw_buffer_load_b128(
+                            rk, (int)(vo + i * 16 * kbytes_row), (int)(kblk * BC * kbytes_row), 0));
     }
 }
 
@@ -105,8 +121,10 @@ __device__ __forceinline__ uint32_t pk_hi(uint32_t x, uint32_t y) {
     return __builtin_amdgcn_perm(y, x, 0x07060302u);
 }
 
-__device__ __forceinline__ void store_stage(const Stage &st, char *Ks, char *Vt, uint32_t tid) {
+__device__ __forceinline__ void store_stage(const Stage &st, char *Ks, char *Vt, bool kval,
+                                            bool vval, uint32_t tid) {
     if (tid < 128) {
+        if (!vval) return;
         const uint32_t v = tid;
         const uint32_t db = v & 7, bp = (v >> 3) & 1, h = (v >> 4) & 1, c = v >> 5;
         // keys 16c + 8b' + 4h + i  ->  position 16c + 8h + 4b' + i: chunk 2c+h, half bp
@@ -128,6 +146,7 @@ __device__ __forceinline__ void store_stage(const Stage &st, char *Ks, char *Vt,
             *(phx_u2 *)(Vt + lds_off(d0 + 1, chunk) + 8 * bp) = hi;
         }
     } else {
+        if (!kval) return;
         const uint32_t u = tid - 128;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -137,6 +156,35 @@ __device__ __forceinline__ void store_stage(const Stage &st, char *Ks, char *Vt,
     }
 }
 
+// S^T = K . Q^T for one key block: sT[t] holds keys 32t + 8(r/4) + 4g + r%4
+// of query lq.
+__device__ __forceinline__ void scores(phx_f16v (&sT)[2], const phx_h8 (&kf)[2][4],
+                                       const phx_h8 (&qf)[4]) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        sT[t] = (phx_f16v){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+            sT[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[t][s], qf[s], sT[t], 0, 0, 0);
+    }
+}
+
+__device__ __forceinline__ void read_k(phx_h8 (&kf)[2][4], const char *Ks, uint32_t lq,
+                                       uint32_t g) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+            kf[t][s] = *(const phx_h8 *)(Ks + lds_off(32 * t + lq, 2 * s + g));
+}
+
+// The running max is raised only when a row's block max exceeds it by more
+// than RESCALE_SLACK (in log2 units), so the O/l rescale (32 multiplies) is
+// skipped on almost every block; p = exp2(s*c - m) then stays <= 2^8, which
+// f16 P and f32 l hold exactly as well as the reference's per-block update.
+// O = acc / l is the same quantity either way.
+#define RESCALE_SLACK 8.0f
+
 __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp, T *O,
                                             int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo,
                                             uint32_t Nk, uint32_t q0, float scale,
@@ -145,6 +193,20 @@ __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp
     const uint32_t lq = lane & 31, g = lane >> 5;
     const uint32_t myq = q0 + wave * 32 + lq;
     const float c2 = scale * LOG2E;
+    const uint32_t nkb = Nk / BC;
+
+    // buffer views of this head's K and V
+    const uint32_t kbr = (uint32_t)(ldk * 2), vbr = (uint32_t)(ldv * 2);
+    const __amdgpu_buffer_rsrc_t rk = phx_rsrc(Kp, (uint32_t)((Nk - 1) * kbr + D * 2));
+    const __amdgpu_buffer_rsrc_t rv = phx_rsrc(Vp, (uint32_t)((Nk - 1) * vbr + D * 2));
+    uint32_t vo;
+    if (tid < 128) {
+        const uint32_t v = tid, db = v & 7, bp = (v >> 3) & 1, h = (v >> 4) & 1, c = v >> 5;
+        vo = (16 * c + 8 * bp + 4 * h) * vbr + 16 * db;
+    } else {
+        const uint32_t u = tid - 128;
+        vo = (u >> 3) * kbr + 16 * (u & 7);
+    }
 
     // Q^T operand: s-step s covers d = 16s + 8g .. +7
     phx_h8 qf[4];
@@ -157,37 +219,51 @@ __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp
     float m2 = M_INIT * LOG2E;
     float l = 0.0f;
 
-    const uint32_t nkb = Nk / BC;
+    // prologue: K_0, V_0 -> buffer 0; K_1 -> buffer 1
     Stage st;
-    load_stage(st, Kp, Vp, ldk, ldv, 0, tid);
-    store_stage(st, lds[0][0], lds[0][1], tid);
+    load_stage(st, rk, rv, kbr, vbr, 0, 0, true, true, vo, tid);
+    store_stage(st, lds[0][0], lds[0][1], true, true, tid);
+    load_stage(st, rk, rv, kbr, vbr, 1, 0, nkb > 1, false, vo, tid);
+    store_stage(st, lds[1][0], lds[1][1], nkb > 1, false, tid);
     __syncthreads();
 
-    for (uint32_t kb = 0; kb < nkb; ++kb) {
-        const uint32_t cur = kb & 1;
-        if (kb + 1 < nkb) load_stage(st, Kp, Vp, ldk, ldv, (kb + 1) * BC, tid);
-        const char *Ks = lds[cur][0];
-        const char *Vt = lds[cur][1];
+    phx_f16v sT[2];
+    {
+        phx_h8 kf[2][4];
+        read_k(kf, lds[0][0], lq, g);
+        scores(sT, kf, qf);
+    }
 
-        // S^T[t]: keys 32t + 8(r/4) + 4g + r%4, query lq
-        phx_f16v sT[2];
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            sT[t] = (phx_f16v){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                phx_h8 kf = *(const phx_h8 *)(Ks + lds_off(32 * t + lq, 2 * s + g));
-                sT[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[s], sT[t], 0, 0, 0);
-            }
+    for (uint32_t kb = 0; kb < nkb; ++kb) {
+        const uint32_t cur = kb & 1, nxt = cur ^ 1;
+        const bool more = kb + 1 < nkb;
+        // global loads of K_{kb+2} and V_{kb+1}, stored at the end of this block
+        load_stage(st, rk, rv, kbr, vbr, kb + 2, kb + 1, kb + 2 < nkb, more, vo, tid);
+
+        // next block's scores go to the MFMA pipe while this block's softmax
+        // runs on the VALU
+        phx_f16v sN[2];
+        {
+            phx_h8 kf[2][4];
+            if (more) read_k(kf, lds[nxt][0], lq, g);
+            if (more) scores(sN, kf, qf);
         }
+        __builtin_amdgcn_sched_barrier(0);
+
         float mx = sT[0][0];
 #pragma unroll
         for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sT[0][r]);
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sT[1][r]);
-        mx = fmaxf(mx, shfl_xor32(mx));
-        const float m2new = fmaxf(m2, mx * c2);
-        const float corr = __builtin_amdgcn_exp2f(m2 - m2new);
+        mx = fmaxf(mx, shfl_xor32(mx)) * c2;
+        if (__ballot(mx > m2 + RESCALE_SLACK)) {  // wave-uniform
+            const float m2new = fmaxf(m2, mx);
+            const float corr = __builtin_amdgcn_exp2f(m2 - m2new);
+            l = l * corr;
+            acc[0] = acc[0] * corr;
+            acc[1] = acc[1] * corr;
+            m2 = m2new;
+        }
         float ps = 0.0f;
         phx_h8 pf[4];
 #pragma unroll
@@ -197,27 +273,30 @@ __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp
                 phx_h8 v;
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sT[t][8 * hh + j], c2, -m2new));
+                    const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sT[t][8 * hh + j], c2, -m2));
                     ps += p;
                     v[j] = (_Float16)p;
                 }
                 pf[2 * t + hh] = v;
             }
         ps += shfl_xor32(ps);
-        l = l * corr + ps;
-        m2 = m2new;
-        acc[0] = acc[0] * corr;
-        acc[1] = acc[1] * corr;
+        l = l + ps;
         // O^T[dt] += V^T[dt rows, 16 keys of block c] . P^T
+        const char *Vt = lds[cur][1];
 #pragma unroll
         for (int c = 0; c < 4; ++c)
 #pragma unroll
             for (int dt = 0; dt < 2; ++dt) {
-                phx_h8 vf = *(const phx_h8 *)(Vt + lds_off(32 * dt + lq, 2 * c + g));
+                const phx_h8 vf = *(const phx_h8 *)(Vt + lds_off(32 * dt + lq, 2 * c + g));
                 acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[c], acc[dt], 0, 0, 0);
             }
-
-        if (kb + 1 < nkb) store_stage(st, lds[cur ^ 1][0], lds[cur ^ 1][1], tid);
+        if (more) {
+            sT[0] = sN[0];
+            sT[1] = sN[1];
+        }
+        // K_{kb+2} -> buffer cur (its K_kb was used for the scores one block
+        // ago); V_{kb+1} -> buffer nxt (its V_{kb-1} is done).
+        store_stage(st, lds[cur][0], lds[nxt][1], kb + 2 < nkb, more, tid);
         __syncthreads();
     }
 
@@ -386,7 +465,7 @@ __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp
 }
 #endif
 
-extern "C" __global__ __launch_bounds__(NT) void flash_attention(PHX_MEMREF2(T, q, int64_t),
+extern "C" __global__ __launch_bounds__(NT, FA_MIN_BLOCKS) void flash_attention(PHX_MEMREF2(T, q, int64_t),
                                                                   PHX_MEMREF2(T, k, int64_t),
                                                                   PHX_MEMREF2(T, v, int64_t),
                                                                   PHX_MEMREF2(T, o, int64_t),
@@ -403,7 +482,7 @@ extern "C" __global__ __launch_bounds__(NT) void flash_attention(PHX_MEMREF2(T, 
                     v_st0, o_st0, (uint32_t)Nk, rb * BR, scale, lds);
 }
 
-extern "C" __global__ __launch_bounds__(NT) void flash_attention_bh(PHX_MEMREF3(T, q, int64_t),
+extern "C" __global__ __launch_bounds__(NT, FA_MIN_BLOCKS) void flash_attention_bh(PHX_MEMREF3(T, q, int64_t),
                                                                      PHX_MEMREF3(T, k, int64_t),
                                                                      PHX_MEMREF3(T, v, int64_t),
                                                                      PHX_MEMREF3(T, o, int64_t),

@@ -19,25 +19,29 @@
 // differs from the reference only in the sign of an exactly-zero result.
 //
 // MI355X design
-//   * 256x256 output tile per workgroup, 256 threads = 4 waves (2x2), each wave
-//     a 128x128 sub-tile = 4x4 v_mfma_f32_32x32x16_f16 tiles whose 256 f32
-//     accumulators live in AGPRs.  At 4096^3 this is 256 tiles: one per CU.
-//   * K step 64.  A is staged as As[m][k], B transposed to Bs[n][k], so every
-//     MFMA operand is one ds_read_b128 (8 consecutive k of one row/column).
-//     Rows are 128 bytes; the 16-byte chunk index is XOR-swizzled with
-//     ((row >> 1) & 7): gfx950's LDS serves 64 banks (256 bytes) per clock, so
-//     the 16 lanes of a 16-byte access must land in 16 distinct slots of a
-//     256-byte line, which makes the staging writes and operand reads
-//     conflict free (SQ_LDS_BANK_CONFLICT was a third of LDS cycles with a
-//     32-bank swizzle).
-//   * B (row-major [K,N]) is transposed in registers: each thread loads an 8x8
-//     block (8 rows of 16 bytes) and re-packs it with v_perm into 8 k-runs.
-//   * LDS double buffer (2 x 64 KiB); the next K step's global loads are in
-//     flight while the current step's 64 MFMAs per wave run; one barrier per
-//     K step.
-//   * Workgroups are renumbered XCD-major and grouped 4 tile-rows deep so the
-//     32 workgroups of one XCD cover a 4x8 block of tiles and share A/B panels
-//     in that XCD's L2.
+//   * 256x128 output tile, K step 32, 256 threads = 4 waves (2x2) of 128x64,
+//     each 4x2 v_mfma_f32_32x32x16_f16 tiles (128 f32 accumulators).  LDS is
+//     2 x 24 KiB and a wave stays under 256 registers, so two workgroups share
+//     each CU and cover each other's barrier, LDS and global-load stalls
+//     (at 4096^2: 512 tiles, two per CU, all resident at once).
+//   * A is staged As[m][k] (64-byte rows); an MFMA A operand (8 consecutive k
+//     of one row) is one ds_read_b128.  B stays row-major Bs[k][n] (256-byte
+//     rows) and its operand is read with gfx950's transposing
+//     ds_read_b64_tr_b16: in a 16-lane group, lane s supplies 4 halves of row
+//     k0 + s/4 at column n0 + 4*(s%4), and lane i receives B[k0..k0+3][n0+i].
+//     Two such reads give a lane its 8 consecutive k.  Staging is therefore a
+//     plain 16-byte copy for both operands.
+//   * gfx950's LDS serves 64 banks (256 bytes) per clock.  The 16-byte chunk
+//     index is XOR-swizzled so every 16-lane (b128) or 32-lane (b64) group
+//     hits distinct banks: As chunk ^ ((row >> 2) & 3), Bs chunk ^ 4*(row % 4).
+//   * Global loads are buffer loads off a per-K-step scalar base; the next
+//     step's loads are in flight while the current step's 16 MFMAs per wave
+//     run; one barrier per step.  The next K slice's LDS reads are issued
+//     ahead of the current slice's MFMAs (fenced, since the wave issues in
+//     order).
+//   * Workgroups are renumbered XCD-major and grouped 8 tile-rows deep, so the
+//     64 workgroups of one XCD cover an 8x8 block of tiles and share A/B
+//     panels in that XCD's L2.
 #include "phx_common.h"
 
 #ifdef PHX_GEMM_TC
@@ -48,40 +52,30 @@ typedef _Float16 TIn;
 typedef _Float16 TOut;
 #endif
 
-#define BM PHX_H_BM
-#define BN PHX_H_BN
-#define BK PHX_H_BK
+#define BM PHX_H_BM  // 256
+#define BN PHX_H_BN  // 128
+#define BK PHX_H_BK  // 32
 #define NT PHX_H_THREADS
 #define WM 128  // wave tile rows
-#define WN 128  // wave tile cols
-#define GROUP_M 4
-// Prefetch distance in K steps: two register stages for f16 inputs (64
-// VGPRs each); the f32 inputs of the tc variant need 128 VGPRs per stage, so
-// it keeps one.
-#ifdef PHX_GEMM_TC
-#define PREFETCH 1
-#else
-#define PREFETCH 2
-#endif
+#define WN 64   // wave tile cols
+#define GROUP_M 8
 
-// LDS: [buffer][row][64 halves], 16-byte chunks swizzled by (row & 7).
-#define LDS_ROW_BYTES (BK * 2)
-#define LDS_TILE_BYTES (BM * LDS_ROW_BYTES)
+#define A_ROW_BYTES (BK * 2)             // 64
+#define B_ROW_BYTES (BN * 2)             // 256
+#define A_BYTES (BM * A_ROW_BYTES)       // 16 KiB
+#define B_BYTES (BK * B_ROW_BYTES)       // 8 KiB
+#define STAGE_BYTES (A_BYTES + B_BYTES)  // 24 KiB
+#define EP_PITCH 68                      // epilogue LDS row pitch (floats)
 
-__device__ __forceinline__ uint32_t lds_off(uint32_t row, uint32_t chunk) {
-    return row * LDS_ROW_BYTES + ((chunk ^ ((row >> 1) & 7)) << 4);
+typedef __fp16 phx_fp16x4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
+typedef __attribute__((address_space(3))) phx_fp16x4 *phx_lds_h4p;
+
+__device__ __forceinline__ uint32_t a_off(uint32_t row, uint32_t chunk) {
+    return row * A_ROW_BYTES + ((chunk ^ ((row >> 2) & 3)) << 4);
 }
-
-// Global loads of one K step, held in registers until written to LDS.
-struct Stage {
-#ifdef PHX_GEMM_TC
-    phx_f4 a[8][2];  // 8 row-chunks, each 8 floats
-    phx_f4 b[8][2];  // 8 rows of the 8x8 block, each 8 floats
-#else
-    phx_u4 a[8];     // 8 row-chunks of 8 halves
-    phx_u4 b[8];     // 8 rows of the 8x8 block, 8 halves each
-#endif
-};
+__device__ __forceinline__ uint32_t b_off(uint32_t row, uint32_t chunk) {
+    return row * B_ROW_BYTES + ((chunk ^ ((row & 3) << 2)) << 4);
+}
 
 // Buffer resource over `bytes` bytes from p (gfx9 dword3 = 0x00020000).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t phx_rsrc(const void *p, uint32_t bytes) {
@@ -94,26 +88,30 @@ __device__ __forceinline__ V buf_load(__amdgpu_buffer_rsrc_t r, uint32_t voff, u
     return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
 }
 
-// One K step of A (BM x BK at row m0, col k0) and B (BK x BN at row k0,
-// col n0).  The buffer bases move with k0, so every per-lane offset is a
-// small 32-bit VGPR constant and the per-load offsets are scalars.
-//   A: row = i*32 + tid/8, 8 k values at chunk tid%8
-//   B: 8x8 block, rows k0 + 8*(tid%8) + i, cols n0 + 8*(tid/8) .. +7
+// Global loads of one K step.  Thread t stages
+//   A: rows i*64 + t/4 (i < 4), 16-byte chunk t%4 (8 k values);
+//   B: rows t/16 and t/16 + 16, chunk t%16 (8 n values).
+struct Stage {
+#ifdef PHX_GEMM_TC
+    phx_f4 a[4][2];
+    phx_f4 b[2][2];
+#else
+    phx_u4 a[4];
+    phx_u4 b[2];
+#endif
+};
+
 __device__ __forceinline__ void load_stage(Stage &st, const TIn *A, int64_t lda, const TIn *B,
                                            int64_t ldb, uint32_t m0, uint32_t n0, uint32_t k0,
-                                           uint32_t voa, uint32_t vob, bool valid) {
-    // A step past K (the padding step of an odd step count) gets empty
-    // buffer ranges: out-of-range buffer loads return zeros.
+                                           uint32_t voa, uint32_t vob) {
     const uint32_t esz = sizeof(TIn);
     const __amdgpu_buffer_rsrc_t ra =
-        phx_rsrc(A + (int64_t)m0 * lda + (valid ? k0 : 0),
-                 valid ? (uint32_t)((BM - 1) * lda + BK) * esz : 0u);
+        phx_rsrc(A + (int64_t)m0 * lda + k0, (uint32_t)((BM - 1) * lda + BK) * esz);
     const __amdgpu_buffer_rsrc_t rb =
-        phx_rsrc(B + (int64_t)(valid ? k0 : 0) * ldb + n0,
-                 valid ? (uint32_t)((BK - 1) * ldb + BN) * esz : 0u);
+        phx_rsrc(B + (int64_t)k0 * ldb + n0, (uint32_t)((BK - 1) * ldb + BN) * esz);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const uint32_t so = (uint32_t)(i * 32 * lda) * esz;
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t so = (uint32_t)(i * 64 * lda) * esz;
 #ifdef PHX_GEMM_TC
         st.a[i][0] = buf_load<phx_f4>(ra, voa, so);
         st.a[i][1] = buf_load<phx_f4>(ra, voa + 16, so);
@@ -122,8 +120,8 @@ __device__ __forceinline__ void load_stage(Stage &st, const TIn *A, int64_t lda,
 #endif
     }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const uint32_t so = (uint32_t)(i * ldb) * esz;
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t so = (uint32_t)(i * 16 * ldb) * esz;
 #ifdef PHX_GEMM_TC
         st.b[i][0] = buf_load<phx_f4>(rb, vob, so);
         st.b[i][1] = buf_load<phx_f4>(rb, vob + 16, so);
@@ -133,125 +131,88 @@ __device__ __forceinline__ void load_stage(Stage &st, const TIn *A, int64_t lda,
     }
 }
 
-#ifndef PHX_GEMM_TC
-// Selects the low (hi=0) or high (hi=1) halves of two dwords: {lo16(x), lo16(y)}.
-__device__ __forceinline__ uint32_t pk_lo(uint32_t x, uint32_t y) {
-    return __builtin_amdgcn_perm(y, x, 0x05040100u);
-}
-__device__ __forceinline__ uint32_t pk_hi(uint32_t x, uint32_t y) {
-    return __builtin_amdgcn_perm(y, x, 0x07060302u);
+#ifdef PHX_GEMM_TC
+__device__ __forceinline__ phx_u4 to_h8(const phx_f4 &lo, const phx_f4 &hi) {
+    phx_u4 v;
+    v.x = phx_pack_h2(lo.x, lo.y);
+    v.y = phx_pack_h2(lo.z, lo.w);
+    v.z = phx_pack_h2(hi.x, hi.y);
+    v.w = phx_pack_h2(hi.z, hi.w);
+    return v;
 }
 #endif
 
-__device__ __forceinline__ void store_stage(const Stage &st, char *As, char *Bs, uint32_t tid) {
-    const uint32_t ar = tid >> 3, ac = tid & 7;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-#ifdef PHX_GEMM_TC
-        phx_u4 v;
-        v.x = phx_pack_h2(st.a[i][0].x, st.a[i][0].y);
-        v.y = phx_pack_h2(st.a[i][0].z, st.a[i][0].w);
-        v.z = phx_pack_h2(st.a[i][1].x, st.a[i][1].y);
-        v.w = phx_pack_h2(st.a[i][1].z, st.a[i][1].w);
-#else
-        phx_u4 v = st.a[i];
-#endif
-        *(phx_u4 *)(As + lds_off(i * 32 + ar, ac)) = v;
-    }
-    // Transpose the 8x8 block: output column j (n = 8*bn + j) holds
-    // k = 8*bk .. 8*bk+7.
-    const uint32_t bk = tid & 7, bn = tid >> 3;
-#ifdef PHX_GEMM_TC
-    float e[8][8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        e[i][0] = st.b[i][0].x; e[i][1] = st.b[i][0].y; e[i][2] = st.b[i][0].z; e[i][3] = st.b[i][0].w;
-        e[i][4] = st.b[i][1].x; e[i][5] = st.b[i][1].y; e[i][6] = st.b[i][1].z; e[i][7] = st.b[i][1].w;
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        phx_u4 v;
-        v.x = phx_pack_h2(e[0][j], e[1][j]);
-        v.y = phx_pack_h2(e[2][j], e[3][j]);
-        v.z = phx_pack_h2(e[4][j], e[5][j]);
-        v.w = phx_pack_h2(e[6][j], e[7][j]);
-        *(phx_u4 *)(Bs + lds_off(bn * 8 + j, bk)) = v;
-    }
-#else
-    // row i dword d holds halves (n=2d, n=2d+1).  Column j=2d+h of rows
-    // (i, i+1) packs as pk_lo/pk_hi of dword d of those rows.
-    uint32_t r[8][4];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        r[i][0] = st.b[i].x; r[i][1] = st.b[i].y; r[i][2] = st.b[i].z; r[i][3] = st.b[i].w;
-    }
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-        phx_u4 lo, hi;
-        lo.x = pk_lo(r[0][d], r[1][d]); hi.x = pk_hi(r[0][d], r[1][d]);
-        lo.y = pk_lo(r[2][d], r[3][d]); hi.y = pk_hi(r[2][d], r[3][d]);
-        lo.z = pk_lo(r[4][d], r[5][d]); hi.z = pk_hi(r[4][d], r[5][d]);
-        lo.w = pk_lo(r[6][d], r[7][d]); hi.w = pk_hi(r[6][d], r[7][d]);
-        *(phx_u4 *)(Bs + lds_off(bn * 8 + 2 * d, bk)) = lo;
-        *(phx_u4 *)(Bs + lds_off(bn * 8 + 2 * d + 1, bk)) = hi;
-    }
-#endif
-}
-
-// One K step: compute from LDS buffer `cur`; issue the loads of step kt+2
-// into `mine` (free: its previous contents were stored at the end of step
-// kt-1); at the end store `next` (step kt+1, loaded during step kt-1) into
-// LDS buffer `nxt`.
-__device__ __forceinline__ void k_step(phx_f16v (&acc)[4][4], Stage &mine, Stage &next,
-                                       const TIn *A, int64_t lda, const TIn *B, int64_t ldb,
-                                       uint32_t m0, uint32_t n0, uint32_t kt, uint32_t nk,
-                                       uint32_t nkv, uint32_t voa, uint32_t vob, char (*cur)[LDS_TILE_BYTES],
-                                       char (*nxt)[LDS_TILE_BYTES], uint32_t wm, uint32_t wn,
-                                       uint32_t lrow, uint32_t lgrp, uint32_t tid) {
-    const char *As = cur[0];
-    const char *Bs = cur[1];
-    phx_h8 af[2][4], bf[2][4];
+__device__ __forceinline__ void store_stage(const Stage &st, char *stage, uint32_t tid) {
+    char *As = stage, *Bs = stage + A_BYTES;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        af[0][i] = *(const phx_h8 *)(As + lds_off(wm + i * 32 + lrow, lgrp));
-        bf[0][i] = *(const phx_h8 *)(Bs + lds_off(wn + i * 32 + lrow, lgrp));
+#ifdef PHX_GEMM_TC
+        const phx_u4 v = to_h8(st.a[i][0], st.a[i][1]);
+#else
+        const phx_u4 v = st.a[i];
+#endif
+        *(phx_u4 *)(As + a_off(i * 64 + (tid >> 2), tid & 3)) = v;
     }
-    if (kt + PREFETCH < nk)
-        load_stage(mine, A, lda, B, ldb, m0, n0, (kt + PREFETCH) * BK, voa, vob,
-                   kt + PREFETCH < nkv);
-    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (uint32_t s = 0; s < BK / 16; ++s) {
-        const uint32_t b = s & 1;
-        // The wave issues in order: the next slice's LDS reads go out ahead
-        // of this slice's 16 MFMAs (fenced so the scheduler keeps them
-        // there), so their latency hides under the MFMAs.
-        if (s + 1 < BK / 16) {
-            const uint32_t chunk = 2 * (s + 1) + lgrp;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                af[b ^ 1][i] = *(const phx_h8 *)(As + lds_off(wm + i * 32 + lrow, chunk));
-                bf[b ^ 1][i] = *(const phx_h8 *)(Bs + lds_off(wn + i * 32 + lrow, chunk));
-            }
-        }
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                acc[i][j] =
-                    __builtin_amdgcn_mfma_f32_32x32x16_f16(af[b][i], bf[b][j], acc[i][j], 0, 0, 0);
-        __builtin_amdgcn_sched_barrier(0);
+    for (int i = 0; i < 2; ++i) {
+#ifdef PHX_GEMM_TC
+        const phx_u4 v = to_h8(st.b[i][0], st.b[i][1]);
+#else
+        const phx_u4 v = st.b[i];
+#endif
+        *(phx_u4 *)(Bs + b_off(i * 16 + (tid >> 4), tid & 15)) = v;
     }
-    if (kt + 1 < nk) store_stage(next, nxt[0], nxt[1], tid);
-    __syncthreads();
 }
 
-extern "C" __global__ __launch_bounds__(NT, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm(PHX_MEMREF2(TIn, a, int64_t),
+struct Frags {
+    phx_h8 a[4];
+    phx_h8 b[2];
+};
+
+// Operands of K slice s (k = 16s .. 16s+15) for this wave.
+//   A: lane l reads row wm + 32i + l%32, k = 16s + 8*(l/32) .. +7.
+//   B: lane l needs column wn + 32j + l%32 at the same 8 k; two transposing
+//      reads (k +0..3, +4..7) from the lane's 16-lane group q = l/16, which
+//      covers columns 16*(q%2) .. +15 and k half q/2.
+__device__ __forceinline__ void read_frags(Frags &f, const char *stage, uint32_t s, uint32_t wm,
+                                           uint32_t wn, uint32_t lane) {
+    const char *As = stage;
+    const char *Bs = stage + A_BYTES;
+    const uint32_t lrow = lane & 31, g = lane >> 5;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        f.a[i] = *(const phx_h8 *)(As + a_off(wm + i * 32 + lrow, 2 * s + g));
+    const uint32_t q = lane >> 4, sl = lane & 15;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const uint32_t col = wn + j * 32 + 16 * (q & 1) + 4 * (sl & 3);  // halves
+        phx_fp16x4 h[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const uint32_t row = 16 * s + 8 * (q >> 1) + 4 * t + (sl >> 2);
+            const uint32_t off = b_off(row, col >> 3) + ((col & 7) << 1);
+            h[t] = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                (phx_lds_h4p)((__attribute__((address_space(3))) char *)(Bs + off)));
+        }
+        phx_h4 lo = __builtin_bit_cast(phx_h4, h[0]);
+        phx_h4 hi = __builtin_bit_cast(phx_h4, h[1]);
+        f.b[j] = (phx_h8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    }
+}
+
+__device__ __forceinline__ void mfma_slice(phx_f16v (&acc)[4][2], const Frags &f) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
+}
+
+extern "C" __global__ __launch_bounds__(NT, 2) void gemm(PHX_MEMREF2(TIn, a, int64_t),
                                                           PHX_MEMREF2(TIn, b, int64_t),
                                                           PHX_MEMREF2(TOut, c, int64_t),
                                                           float alpha, float beta) {
-    __shared__ __attribute__((aligned(16))) char lds[2][2][LDS_TILE_BYTES];
+    __shared__ __attribute__((aligned(16))) char lds[2][STAGE_BYTES];
 
     const int64_t M = a_s0, K = a_s1, N = b_s1;
     // Uniform preconditions (validated on the host by phx_check_shape; a
@@ -268,26 +229,20 @@ extern "C" __global__ __launch_bounds__(NT, 1) __attribute__((amdgpu_waves_per_e
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63;
     const uint32_t wave = tid >> 6;
-    const uint32_t wm = (wave >> 1) * WM;  // wave row offset in tile
+    const uint32_t wm = (wave >> 1) * WM;
     const uint32_t wn = (wave & 1) * WN;
     const uint32_t tiles_n = (uint32_t)(N / BN);
-    const uint32_t ntiles = (uint32_t)(M / BM) * tiles_n;
+    const uint32_t tiles_m = (uint32_t)(M / BM);
+    const uint32_t ntiles = tiles_m * tiles_n;
     const uint32_t nblk = phx_block_count();
-    // K steps, padded to even: the pipeline runs in pairs of steps, and a
-    // padding step multiplies zeros.
-    const uint32_t nkv = (uint32_t)(K / BK);
-    const uint32_t nk = (nkv + 1) & ~1u;
-
-    const uint32_t lrow = lane & 31;  // MFMA operand row/col within a 32 tile
-    const uint32_t lgrp = lane >> 5;  // k half (0/1) inside a 16-wide k slice
-    // per-lane byte offsets of the staging loads (see load_stage)
-    const uint32_t voa = (uint32_t)(((tid >> 3) * lda + (tid & 7) * 8) * sizeof(TIn));
-    const uint32_t vob = (uint32_t)(((tid & 7) * 8 * ldb + (tid >> 3) * 8) * sizeof(TIn));
+    const uint32_t nk = (uint32_t)(K / BK);
+    const uint32_t lrow = lane & 31, lgrp = lane >> 5;
+    // per-lane byte offsets of the staging loads (see Stage)
+    const uint32_t voa = (uint32_t)(((tid >> 2) * lda + (tid & 3) * 8) * sizeof(TIn));
+    const uint32_t vob = (uint32_t)(((tid >> 4) * ldb + (tid & 15) * 8) * sizeof(TIn));
 
     for (uint32_t t = phx_block_linear(); t < ntiles; t += nblk) {
         const uint32_t ts = nblk == ntiles ? phx_xcd_swizzle(t, ntiles) : t;
-        // grouped ordering: GROUP_M tile-rows per group
-        const uint32_t tiles_m = ntiles / tiles_n;
         const uint32_t gsz = GROUP_M * tiles_n;
         const uint32_t g0 = (ts / gsz) * GROUP_M;
         const uint32_t gm = (tiles_m - g0) < GROUP_M ? (tiles_m - g0) : GROUP_M;
@@ -295,72 +250,83 @@ extern "C" __global__ __launch_bounds__(NT, 1) __attribute__((amdgpu_waves_per_e
         const uint32_t tn = (ts % gsz) / gm;
         const uint32_t m0 = tm * BM, n0 = tn * BN;
 
-        phx_f16v acc[4][4];
+        phx_f16v acc[4][2];
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < 2; ++j)
                 acc[i][j] = (phx_f16v){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 
-        // PREFETCH == 2: the loads of K step t+2 are issued while step t
-        // computes and written to LDS at the end of step t+1, so each load has
-        // two steps of MFMA time to land.  PREFETCH == 1: one stage, loaded
-        // during step t and stored at its end.
-        Stage st0;
-#if PREFETCH == 2
-        Stage st1;
-#else
-        Stage &st1 = st0;
-#endif
-        load_stage(st0, A, lda, B, ldb, m0, n0, 0, voa, vob, true);
-        store_stage(st0, lds[0][0], lds[0][1], tid);
-#if PREFETCH == 2
-        load_stage(st0, A, lda, B, ldb, m0, n0, BK, voa, vob, nkv > 1);
+        Stage st;
+        load_stage(st, A, lda, B, ldb, m0, n0, 0, voa, vob);
+        store_stage(st, lds[0], tid);
         __syncthreads();
-        for (uint32_t kt = 0; kt < nk; kt += 2) {
-            k_step(acc, st1, st0, A, lda, B, ldb, m0, n0, kt, nk, nkv, voa, vob, lds[0], lds[1],
-                   wm, wn, lrow, lgrp, tid);
-            k_step(acc, st0, st1, A, lda, B, ldb, m0, n0, kt + 1, nk, nkv, voa, vob, lds[1],
-                   lds[0], wm, wn, lrow, lgrp, tid);
-        }
-#else
-        __syncthreads();
-        for (uint32_t kt = 0; kt < nk; kt += 2) {
-            k_step(acc, st0, st1, A, lda, B, ldb, m0, n0, kt, nk, nkv, voa, vob, lds[0], lds[1],
-                   wm, wn, lrow, lgrp, tid);
-            k_step(acc, st0, st1, A, lda, B, ldb, m0, n0, kt + 1, nk, nkv, voa, vob, lds[1],
-                   lds[0], wm, wn, lrow, lgrp, tid);
-        }
-#endif
 
-        // Epilogue.  acc[i][j][r]: row = 8*(r/4) + 4*lgrp + r%4, col = lrow.
-        if (beta != 0.0f) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const uint32_t col = n0 + wn + j * 32 + lrow;
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const uint32_t row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * lgrp + (r & 3);
-                        TOut *pc = C + (int64_t)row * ldc + col;
-                        float v = alpha * acc[i][j][r];
-                        float cb = beta * (float)*pc;
-                        *pc = (TOut)(v + cb);
-                    }
-                }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const uint32_t col = n0 + wn + j * 32 + lrow;
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const uint32_t row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * lgrp + (r & 3);
-                        C[(int64_t)row * ldc + col] = (TOut)(alpha * acc[i][j][r]);
-                    }
-                }
+        for (uint32_t kt = 0; kt < nk; ++kt) {
+            const char *cur = lds[kt & 1];
+            Frags f0, f1;
+            read_frags(f0, cur, 0, wm, wn, lane);
+            if (kt + 1 < nk) load_stage(st, A, lda, B, ldb, m0, n0, (kt + 1) * BK, voa, vob);
+            read_frags(f1, cur, 1, wm, wn, lane);
+            __builtin_amdgcn_sched_barrier(0);
+            mfma_slice(acc, f0);
+            __builtin_amdgcn_sched_barrier(0);
+            mfma_slice(acc, f1);
+            __builtin_amdgcn_sched_barrier(0);
+            if (kt + 1 < nk) store_stage(st, lds[(kt + 1) & 1], tid);
+            __syncthreads();
         }
+
+        // Epilogue, staged through LDS so every global access is a 16-byte
+        // row chunk: in pass i each wave parks alpha*acc of its rows
+        // wm+32i .. +31 (32 x 64 floats, row pitch 68 floats so the two lane
+        // halves hit different banks), then reads it back row-wise.
+        // acc[i][j][r] sits at row 8*(r/4) + 4*lgrp + r%4, col 32j + lrow.
+        float *ep = (float *)(&lds[0][0]) + wave * (32 * EP_PITCH);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            __syncthreads();  // the previous pass (or the main loop) is done with LDS
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    ep[(8 * (r >> 2) + 4 * lgrp + (r & 3)) * EP_PITCH + 32 * j + lrow] =
+                        alpha * acc[i][j][r];
+            __syncthreads();
+            // 32 rows x 64 values; a lane moves 8 consecutive values of a row
+            // (8 lanes per row, 8 rows per round, 4 rounds)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const uint32_t row = rr * 8 + (lane >> 3), c8 = (lane & 7) * 8;
+                const float *src = ep + row * EP_PITCH + c8;
+                const phx_f4 v0 = *(const phx_f4 *)src, v1 = *(const phx_f4 *)(src + 4);
+                TOut *dst = C + (int64_t)(m0 + wm + 32 * i + row) * ldc + n0 + wn + c8;
+#ifdef PHX_GEMM_TC
+                phx_f4 o0 = v0, o1 = v1;
+                if (beta != 0.0f) {
+                    const phx_f4 c0 = *(const phx_f4 *)dst, c1 = *(const phx_f4 *)(dst + 4);
+                    o0 = v0 + beta * c0;
+                    o1 = v1 + beta * c1;
+                }
+                *(phx_f4 *)dst = o0;
+                *(phx_f4 *)(dst + 4) = o1;
+#else
+                float o[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+                if (beta != 0.0f) {
+                    const phx_h8 c = *(const phx_h8 *)dst;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const float cb = beta * (float)c[e];
+                        o[e] = o[e] + cb;
+                    }
+                }
+                phx_h8 h;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) h[e] = (_Float16)o[e];
+                *(phx_h8 *)dst = h;
+#endif
+            }
+        }
+        __syncthreads();  // LDS is reused by the next tile's staging
     }
 }

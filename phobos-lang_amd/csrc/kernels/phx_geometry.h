@@ -9,14 +9,16 @@
 
 // saxpy: 256 threads, each handling PHX_SAXPY_VEC float4 per block step.
 #define PHX_SAXPY_THREADS 256
+#ifndef PHX_SAXPY_VEC
 #define PHX_SAXPY_VEC 4
+#endif
 #define PHX_SAXPY_BLOCK_ELEMS (PHX_SAXPY_THREADS * PHX_SAXPY_VEC * 4)
 
-// f16-operand GEMMs (gemm_fp16, gemm_fp16tc_fp32acc): 256x256 output tile,
-// K step 64, 256 threads = 4 waves in a 2x2 arrangement of 128x128.
+// f16-operand GEMMs (gemm_fp16, gemm_fp16tc_fp32acc): 256x128 output tile,
+// K step 32, 256 threads = 4 waves in a 2x2 arrangement of 128x64.
 #define PHX_H_BM 256
-#define PHX_H_BN 256
-#define PHX_H_BK 64
+#define PHX_H_BN 128
+#define PHX_H_BK 32
 #define PHX_H_THREADS 256
 
 // f32 GEMM (gemm_fp32, cluster matmul): 128x128 output tile, K step 32,

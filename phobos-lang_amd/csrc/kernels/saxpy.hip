@@ -15,6 +15,16 @@
 // misaligned bases fall back to a scalar loop.
 #include "phx_common.h"
 
+// Streaming hints: non-temporal loads/stores keep the single-use stream from
+// evicting other data.
+#ifndef PHX_SAXPY_PLAIN
+#define PHX_LOAD(p) __builtin_nontemporal_load(p)
+#define PHX_STORE(v, p) __builtin_nontemporal_store(v, p)
+#else
+#define PHX_LOAD(p) (*(p))
+#define PHX_STORE(v, p) (*(p) = (v))
+#endif
+
 extern "C" __global__ __launch_bounds__(PHX_SAXPY_THREADS) void saxpy(
     PHX_MEMREF1(float, x, int32_t), PHX_MEMREF1(float, y, int32_t),
     PHX_MEMREF1(float, o, int32_t), float alpha) {
@@ -41,8 +51,8 @@ extern "C" __global__ __launch_bounds__(PHX_SAXPY_THREADS) void saxpy(
             for (int u = 0; u < PHX_SAXPY_VEC; ++u) {
                 const int64_t i = base + (int64_t)u * PHX_SAXPY_THREADS;
                 if (i < nv) {
-                    xr[u] = __builtin_nontemporal_load(xv + i);
-                    yr[u] = __builtin_nontemporal_load(yv + i);
+                    xr[u] = PHX_LOAD(xv + i);
+                    yr[u] = PHX_LOAD(yv + i);
                 }
             }
 #pragma unroll
@@ -51,7 +61,7 @@ extern "C" __global__ __launch_bounds__(PHX_SAXPY_THREADS) void saxpy(
                 if (i < nv) {
                     phx_f4 r = alpha * xr[u];
                     r = r + yr[u];
-                    __builtin_nontemporal_store(r, ov + i);
+                    PHX_STORE(r, ov + i);
                 }
             }
         }
