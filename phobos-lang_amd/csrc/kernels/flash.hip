@@ -77,89 +77,65 @@ __device__ __forceinline__ float shfl_xor32(float v) { return __shfl_xor(v, 32, 
 
 #ifdef PHX_FLASH_F16
 // ---------------------------------------------------------------- f16 path
-// Threads 0-127 stage V^T, threads 128-255 stage K; 4 x 16-byte buffer loads
-// each.  K runs one block ahead of V: during block j the LDS holds K_{j+1}
-// (for the next scores) and V_j (for this block's P.V).
+// K and V are both staged as plain 16-byte row copies (K by threads 128-255,
+// V by threads 0-127, 4 buffer loads each).  K runs one block ahead of V:
+// during block j the LDS holds K_{j+1} (for the next scores) and V_j.
 struct Stage {
     phx_u4 r[4];
 };
+
+typedef __fp16 phx_fp16x4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
+typedef __attribute__((address_space(3))) phx_fp16x4 *phx_lds_h4p;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t phx_rsrc(const void *p, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes,
                                              0x00020000);
 }
 
-// V thread v (0..127): c = v/32 (16-key group), h = (v/16)%2, b' = (v/8)%2,
-// db = v%8: rows key = 16c + 8b' + 4h + i (i<4), d = 8db..8db+7.
-// K thread u (0..127): rows i*16 + u/8 (i<4), 16-byte chunk u%8.
-// vo: this thread's byte offset inside a block (see flash_block).
-__device__ __forceinline__ void load_stage(Stage &st, __amdgpu_buffer_rsrc_t rk,
-                                           __amdgpu_buffer_rsrc_t rv, uint32_t kbytes_row,
-                                           uint32_t vbytes_row, uint32_t kblk, uint32_t vblk,
-                                           bool kval, bool vval, uint32_t vo, uint32_t tid) {
-    if (tid < 128) {
-        if (vval) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                st.r[i] = __builtin_bit_cast(
-                    phx_u4, __builtin_amdgcn_raw_buffer_load_b128(
-                                rv, (int)(vo + i * vbytes_row), (int)(vblk * BC * vbytes_row), 0));
-        }
-    } else if (kval) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            st.r[i] = __builtin_bit_cast(
-                phx_u4, __builtin_amdgcn_raw_buffer_load_b128(
-                            rk, (int)(vo + i * 16 * kbytes_row), (int)(kblk * BC * kbytes_row), 0));
-    }
+// V rows (128 bytes) are read with ds_read_b64_tr_b16: a 32-lane service
+// group touches 4 consecutive rows x 64 bytes, so rows 2 apart are shifted by
+// 64 bytes to land on distinct banks.
+__device__ __forceinline__ uint32_t v_off(uint32_t row, uint32_t chunk) {
+    return row * ROW_BYTES + ((chunk ^ (((row >> 1) & 1) << 2)) << 4);
 }
 
-__device__ __forceinline__ uint32_t pk_lo(uint32_t x, uint32_t y) {
-    return __builtin_amdgcn_perm(y, x, 0x05040100u);
-}
-__device__ __forceinline__ uint32_t pk_hi(uint32_t x, uint32_t y) {
-    return __builtin_amdgcn_perm(y, x, 0x07060302u);
+// Thread u of a 128-thread half stages rows i*16 + u/8 (i < 4), chunk u%8.
+__device__ __forceinline__ void load_stage(Stage &st, __amdgpu_buffer_rsrc_t r, uint32_t rowb,
+                                           uint32_t blk, bool val, uint32_t vo) {
+    if (!val) return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        st.r[i] = __builtin_bit_cast(
+            phx_u4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)(vo + i * 16 * rowb),
+                                                          (int)(blk * BC * rowb), 0));
 }
 
-__device__ __forceinline__ void store_stage(const Stage &st, char *Ks, char *Vt, bool kval,
+__device__ __forceinline__ void store_stage(const Stage &st, char *Ks, char *Vs, bool kval,
                                             bool vval, uint32_t tid) {
+    const uint32_t u = tid & 127, ch = u & 7;
     if (tid < 128) {
         if (!vval) return;
-        const uint32_t v = tid;
-        const uint32_t db = v & 7, bp = (v >> 3) & 1, h = (v >> 4) & 1, c = v >> 5;
-        // keys 16c + 8b' + 4h + i  ->  position 16c + 8h + 4b' + i: chunk 2c+h, half bp
-        const uint32_t chunk = 2 * c + h;
-        uint32_t r[4][4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            r[i][0] = st.r[i].x; r[i][1] = st.r[i].y; r[i][2] = st.r[i].z; r[i][3] = st.r[i].w;
-        }
-#pragma unroll
-        for (int dd = 0; dd < 4; ++dd) {
-            phx_u2 lo, hi;
-            lo.x = pk_lo(r[0][dd], r[1][dd]);
-            lo.y = pk_lo(r[2][dd], r[3][dd]);
-            hi.x = pk_hi(r[0][dd], r[1][dd]);
-            hi.y = pk_hi(r[2][dd], r[3][dd]);
-            const uint32_t d0 = 8 * db + 2 * dd;
-            *(phx_u2 *)(Vt + lds_off(d0, chunk) + 8 * bp) = lo;
-            *(phx_u2 *)(Vt + lds_off(d0 + 1, chunk) + 8 * bp) = hi;
-        }
+        for (int i = 0; i < 4; ++i)
+            *(phx_u4 *)(Vs + v_off(i * 16 + (u >> 3), ch)) = st.r[i];
     } else {
         if (!kval) return;
-        const uint32_t u = tid - 128;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t row = i * 16 + (u >> 3), ch = u & 7;
-            *(phx_u4 *)(Ks + lds_off(row, ch)) = st.r[i];
-        }
+        for (int i = 0; i < 4; ++i)
+            *(phx_u4 *)(Ks + lds_off(i * 16 + (u >> 3), ch)) = st.r[i];
     }
 }
 
 // S^T = K . Q^T for one key block: sT[t] holds keys 32t + 8(r/4) + 4g + r%4
 // of query lq.
-__device__ __forceinline__ void scores(phx_f16v (&sT)[2], const phx_h8 (&kf)[2][4],
-                                       const phx_h8 (&qf)[4]) {
+__device__ __forceinline__ void scores(phx_f16v (&sT)[2], const char *Ks, const phx_h8 (&qf)[4],
+                                       uint32_t lq, uint32_t g) {
+    phx_h8 kf[2][4];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+            kf[t][s] = *(const phx_h8 *)(Ks + lds_off(32 * t + lq, 2 * s + g));
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
         sT[t] = (phx_f16v){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
@@ -169,21 +145,104 @@ __device__ __forceinline__ void scores(phx_f16v (&sT)[2], const phx_h8 (&kf)[2][
     }
 }
 
-__device__ __forceinline__ void read_k(phx_h8 (&kf)[2][4], const char *Ks, uint32_t lq,
-                                       uint32_t g) {
+// The running max is raised only when a row's block max exceeds it by more
+// than RESCALE_SLACK (in log2 units), so the O/l rescale is skipped on almost
+// every block; p = exp2(s*c - m) then stays <= 2^8, which f16 P and f32 l
+// hold as well as the reference's per-block update.  O = acc / l is the same
+// quantity either way.
+#define RESCALE_SLACK 8.0f
+
+struct FlashState {
+    phx_f16v acc[2];
+    float m2, l;
+};
+
+// One key block: issue the next block's scores (K_{kb+1}, MFMA pipe), then
+// this block's softmax (VALU) and P.V (V_kb); stage K_{kb+2} / V_{kb+1}.
+__device__ __forceinline__ void flash_step(FlashState &fs, phx_f16v (&sT)[2], phx_f16v (&sN)[2],
+                                           Stage &st, char (*lds)[2][TILE_BYTES],
+                                           const phx_h8 (&qf)[4], __amdgpu_buffer_rsrc_t rk,
+                                           __amdgpu_buffer_rsrc_t rv, uint32_t kbr, uint32_t vbr,
+                                           uint32_t vo, uint32_t kb, uint32_t nkb, float c2,
+                                           uint32_t tid, uint32_t lane) {
+    const uint32_t lq = lane & 31, g = lane >> 5;
+    const uint32_t cur = kb & 1, nxt = cur ^ 1;
+    const bool more = kb + 1 < nkb;
+    if (tid < 128)
+        load_stage(st, rv, vbr, kb + 1, more, vo);
+    else
+        load_stage(st, rk, kbr, kb + 2, kb + 2 < nkb, vo);
+    if (more) scores(sN, lds[nxt][0], qf, lq, g);
+    __builtin_amdgcn_sched_barrier(0);
+
+    float mx = sT[0][0];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sT[0][r]);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sT[1][r]);
+    mx = fmaxf(mx, shfl_xor32(mx)) * c2;
+    if (__ballot(mx > fs.m2 + RESCALE_SLACK)) {  // wave-uniform
+        const float m2new = fmaxf(fs.m2, mx);
+        const float corr = __builtin_amdgcn_exp2f(fs.m2 - m2new);
+        fs.l = fs.l * corr;
+        fs.acc[0] = fs.acc[0] * corr;
+        fs.acc[1] = fs.acc[1] * corr;
+        fs.m2 = m2new;
+    }
+    // P (f16) and its row sum: v_dot2_f32_f16 against (1, 1) adds the two
+    // f16 values of a pair into an f32 sum.
+    const phx_h2 ones = {(_Float16)1.0f, (_Float16)1.0f};
+    float ps = 0.0f;
+    phx_h8 pf[4];
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
-            kf[t][s] = *(const phx_h8 *)(Ks + lds_off(32 * t + lq, 2 * s + g));
-}
+        for (int hh = 0; hh < 2; ++hh) {
+            phx_h8 v;
+#pragma unroll
+            for (int j = 0; j < 8; j += 2) {
+                const float p0 =
+                    __builtin_amdgcn_exp2f(__builtin_fmaf(sT[t][8 * hh + j], c2, -fs.m2));
+                const float p1 =
+                    __builtin_amdgcn_exp2f(__builtin_fmaf(sT[t][8 * hh + j + 1], c2, -fs.m2));
+                const phx_h2 pp = {(_Float16)p0, (_Float16)p1};
+                ps = __builtin_amdgcn_fdot2(pp, ones, ps, false);
+                v[j] = pp.x;
+                v[j + 1] = pp.y;
+            }
+            pf[2 * t + hh] = v;
+        }
+    ps += shfl_xor32(ps);
+    fs.l = fs.l + ps;
 
-// The running max is raised only when a row's block max exceeds it by more
-// than RESCALE_SLACK (in log2 units), so the O/l rescale (32 multiplies) is
-// skipped on almost every block; p = exp2(s*c - m) then stays <= 2^8, which
-// f16 P and f32 l hold exactly as well as the reference's per-block update.
-// O = acc / l is the same quantity either way.
-#define RESCALE_SLACK 8.0f
+    // O^T[dt] += V^T[32 d rows, 16 keys of block c] . P^T.  The A operand
+    // of lane group g holds keys 16c + 4g + 0..3 and 16c + 8 + 4g + 0..3 (the
+    // order P's registers have), read as two transposing 4-key runs.
+    const char *Vs = lds[cur][1];
+    const uint32_t q = lane >> 4, sl = lane & 15;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt) {
+            const uint32_t col = 32 * dt + 16 * (q & 1) + 4 * (sl & 3);  // d
+            phx_fp16x4 h[2];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const uint32_t row = 16 * c + 8 * t + 4 * (q >> 1) + (sl >> 2);  // key
+                const uint32_t off = v_off(row, col >> 3) + ((col & 7) << 1);
+                h[t] = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                    (phx_lds_h4p)((__attribute__((address_space(3))) char *)(Vs + off)));
+            }
+            const phx_h4 lo = __builtin_bit_cast(phx_h4, h[0]);
+            const phx_h4 hi = __builtin_bit_cast(phx_h4, h[1]);
+            const phx_h8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            fs.acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[c], fs.acc[dt], 0, 0, 0);
+        }
+    // K_{kb+2} -> buffer cur (its K_kb fed the scores one block ago);
+    // V_{kb+1} -> buffer nxt (its V_{kb-1} is done).
+    store_stage(st, lds[cur][0], lds[nxt][1], kb + 2 < nkb, more, tid);
+    __syncthreads();
+}
 
 __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp, T *O,
                                             int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo,
@@ -195,110 +254,46 @@ __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp
     const float c2 = scale * LOG2E;
     const uint32_t nkb = Nk / BC;
 
-    // buffer views of this head's K and V
+    // buffer views of this head's K and V; vo = this thread's staging offset
     const uint32_t kbr = (uint32_t)(ldk * 2), vbr = (uint32_t)(ldv * 2);
     const __amdgpu_buffer_rsrc_t rk = phx_rsrc(Kp, (uint32_t)((Nk - 1) * kbr + D * 2));
     const __amdgpu_buffer_rsrc_t rv = phx_rsrc(Vp, (uint32_t)((Nk - 1) * vbr + D * 2));
-    uint32_t vo;
-    if (tid < 128) {
-        const uint32_t v = tid, db = v & 7, bp = (v >> 3) & 1, h = (v >> 4) & 1, c = v >> 5;
-        vo = (16 * c + 8 * bp + 4 * h) * vbr + 16 * db;
-    } else {
-        const uint32_t u = tid - 128;
-        vo = (u >> 3) * kbr + 16 * (u & 7);
-    }
+    const uint32_t u = tid & 127;
+    const uint32_t vo = (u >> 3) * (tid < 128 ? vbr : kbr) + 16 * (u & 7);
 
     // Q^T operand: s-step s covers d = 16s + 8g .. +7
     phx_h8 qf[4];
 #pragma unroll
     for (int s = 0; s < 4; ++s) qf[s] = *(const phx_h8 *)(Q + (int64_t)myq * ldq + 16 * s + 8 * g);
 
-    phx_f16v acc[2];
-    acc[0] = (phx_f16v){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-    acc[1] = acc[0];
-    float m2 = M_INIT * LOG2E;
-    float l = 0.0f;
+    FlashState fs;
+    fs.acc[0] = (phx_f16v){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    fs.acc[1] = fs.acc[0];
+    fs.m2 = M_INIT * LOG2E;
+    fs.l = 0.0f;
 
-    // prologue: K_0, V_0 -> buffer 0; K_1 -> buffer 1
+    // prologue: V_0 -> buffer 0 (threads 0-127), K_0 -> buffer 0 then K_1 ->
+    // buffer 1 (threads 128-255)
     Stage st;
-    load_stage(st, rk, rv, kbr, vbr, 0, 0, true, true, vo, tid);
-    store_stage(st, lds[0][0], lds[0][1], true, true, tid);
-    load_stage(st, rk, rv, kbr, vbr, 1, 0, nkb > 1, false, vo, tid);
-    store_stage(st, lds[1][0], lds[1][1], nkb > 1, false, tid);
+    if (tid < 128) {
+        load_stage(st, rv, vbr, 0, true, vo);
+        store_stage(st, lds[0][0], lds[0][1], false, true, tid);
+    } else {
+        load_stage(st, rk, kbr, 0, true, vo);
+        store_stage(st, lds[0][0], lds[0][1], true, false, tid);
+        load_stage(st, rk, kbr, 1, nkb > 1, vo);
+        store_stage(st, lds[1][0], lds[1][1], nkb > 1, false, tid);
+    }
     __syncthreads();
 
-    phx_f16v sT[2];
-    {
-        phx_h8 kf[2][4];
-        read_k(kf, lds[0][0], lq, g);
-        scores(sT, kf, qf);
+    phx_f16v s0[2], s1[2];
+    scores(s0, lds[0][0], qf, lq, g);
+    uint32_t kb = 0;
+    for (; kb + 1 < nkb; kb += 2) {
+        flash_step(fs, s0, s1, st, lds, qf, rk, rv, kbr, vbr, vo, kb, nkb, c2, tid, lane);
+        flash_step(fs, s1, s0, st, lds, qf, rk, rv, kbr, vbr, vo, kb + 1, nkb, c2, tid, lane);
     }
-
-    for (uint32_t kb = 0; kb < nkb; ++kb) {
-        const uint32_t cur = kb & 1, nxt = cur ^ 1;
-        const bool more = kb + 1 < nkb;
-        // global loads of K_{kb+2} and V_{kb+1}, stored at the end of this block
-        load_stage(st, rk, rv, kbr, vbr, kb + 2, kb + 1, kb + 2 < nkb, more, vo, tid);
-
-        // next block's scores go to the MFMA pipe while this block's softmax
-        // runs on the VALU
-        phx_f16v sN[2];
-        {
-            phx_h8 kf[2][4];
-            if (more) read_k(kf, lds[nxt][0], lq, g);
-            if (more) scores(sN, kf, qf);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-
-        float mx = sT[0][0];
-#pragma unroll
-        for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sT[0][r]);
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sT[1][r]);
-        mx = fmaxf(mx, shfl_xor32(mx)) * c2;
-        if (__ballot(mx > m2 + RESCALE_SLACK)) {  // wave-uniform
-            const float m2new = fmaxf(m2, mx);
-            const float corr = __builtin_amdgcn_exp2f(m2 - m2new);
-            l = l * corr;
-            acc[0] = acc[0] * corr;
-            acc[1] = acc[1] * corr;
-            m2 = m2new;
-        }
-        float ps = 0.0f;
-        phx_h8 pf[4];
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-                phx_h8 v;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sT[t][8 * hh + j], c2, -m2));
-                    ps += p;
-                    v[j] = (_Float16)p;
-                }
-                pf[2 * t + hh] = v;
-            }
-        ps += shfl_xor32(ps);
-        l = l + ps;
-        // O^T[dt] += V^T[dt rows, 16 keys of block c] . P^T
-        const char *Vt = lds[cur][1];
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-#pragma unroll
-            for (int dt = 0; dt < 2; ++dt) {
-                const phx_h8 vf = *(const phx_h8 *)(Vt + lds_off(32 * dt + lq, 2 * c + g));
-                acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[c], acc[dt], 0, 0, 0);
-            }
-        if (more) {
-            sT[0] = sN[0];
-            sT[1] = sN[1];
-        }
-        // K_{kb+2} -> buffer cur (its K_kb was used for the scores one block
-        // ago); V_{kb+1} -> buffer nxt (its V_{kb-1} is done).
-        store_stage(st, lds[cur][0], lds[nxt][1], kb + 2 < nkb, more, tid);
-        __syncthreads();
-    }
+    if (kb < nkb) flash_step(fs, s0, s1, st, lds, qf, rk, rv, kbr, vbr, vo, kb, nkb, c2, tid, lane);
 
     // acc[dt][r]: d = 32dt + 8(r/4) + 4g + r%4, query lq.
     T *orow = O + (int64_t)myq * ldo;
@@ -308,7 +303,7 @@ __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp
         for (int b = 0; b < 4; ++b) {
             phx_h4 v;
 #pragma unroll
-            for (int rr = 0; rr < 4; ++rr) v[rr] = (_Float16)(acc[dt][4 * b + rr] / l);
+            for (int rr = 0; rr < 4; ++rr) v[rr] = (_Float16)(fs.acc[dt][4 * b + rr] / fs.l);
             *(phx_h4 *)(orow + 32 * dt + 8 * b + 4 * g) = v;
         }
 }
