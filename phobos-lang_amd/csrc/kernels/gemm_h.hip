@@ -21,8 +21,8 @@
 // MI355X design
 //   * 256x128 output tile, K step 32, 256 threads = 4 waves (2x2) of 128x64,
 //     each 4x2 v_mfma_f32_32x32x16_f16 tiles (128 f32 accumulators).  LDS is
-//     2 x 24 KiB and a wave stays under 256 registers, so two workgroups share
-//     each CU and cover each other's barrier, LDS and global-load stalls
+//     72 KiB (f16) / 48 KiB (tc) and a wave stays under 256 registers, so two
+//     workgroups share each CU and cover each other's barrier, LDS and load stalls
 //     (at 4096^2: 512 tiles, two per CU, all resident at once).
 //   * A is staged As[m][k] (64-byte rows); an MFMA A operand (8 consecutive k
 //     of one row) is one ds_read_b128.  B stays row-major Bs[k][n] (256-byte
@@ -34,11 +34,13 @@
 //   * gfx950's LDS serves 64 banks (256 bytes) per clock.  The 16-byte chunk
 //     index is XOR-swizzled so every 16-lane (b128) or 32-lane (b64) group
 //     hits distinct banks: As chunk ^ ((row >> 2) & 3), Bs chunk ^ 4*(row % 4).
-//   * Global loads are buffer loads off a per-K-step scalar base; the next
-//     step's loads are in flight while the current step's 16 MFMAs per wave
-//     run; one barrier per step.  The next K slice's LDS reads are issued
-//     ahead of the current slice's MFMAs (fenced, since the wave issues in
-//     order).
+//   * f16 inputs are copied global -> LDS directly (buffer_load ... lds, no
+//     VGPR staging) into a ring of three 24 KiB stages: K step t+2 is in
+//     flight while step t computes; each wave waits for its own copies
+//     (vmcnt) before the raw barrier that publishes a stage.  The tc variant
+//     (f32 inputs, converted to f16 on the way) stages through registers with
+//     a double-buffered LDS.  Both issue a K slice's LDS reads ahead of its
+//     MFMAs (fenced, since the wave issues in order).
 //   * Workgroups are renumbered XCD-major and grouped 8 tile-rows deep, so the
 //     64 workgroups of one XCD cover an 8x8 block of tiles and share A/B
 //     panels in that XCD's L2.
@@ -208,11 +210,138 @@ __device__ __forceinline__ void mfma_slice(phx_f16v (&acc)[4][2], const Frags &f
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
 }
 
+// Epilogue, staged through LDS so every global access is a 16-byte row
+// chunk: each pass parks alpha*acc for RP rows of every wave's tile in `ep`
+// (row pitch EP_PITCH floats, so the two lane halves hit different banks) and
+// reads it back row-wise.  acc[i][j][r] sits at tile row 32i + 8*(r/4) +
+// 4*lgrp + r%4, column 32j + lrow.  Uses 4 * RP * EP_PITCH * 4 bytes of LDS.
+template <int RP>
+__device__ __forceinline__ void epilogue(const phx_f16v (&acc)[4][2], float *ep_all, TOut *C,
+                                         int64_t ldc, uint32_t m0, uint32_t n0, uint32_t wm,
+                                         uint32_t wn, float alpha, float beta, uint32_t wave,
+                                         uint32_t lane) {
+    const uint32_t lrow = lane & 31, lgrp = lane >> 5;
+    float *ep = ep_all + wave * (RP * EP_PITCH);
+#pragma unroll
+    for (int pass = 0; pass < WM / RP; ++pass) {
+        __syncthreads();  // the previous pass (or the main loop) is done with LDS
+        const int i = (pass * RP) / 32;
+        const int r0 = ((pass * RP) % 32) / 2;  // first accumulator register of this pass
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = r0; r < r0 + RP / 2; ++r)
+                ep[(8 * (r >> 2) + 4 * lgrp + (r & 3) - 2 * r0) * EP_PITCH + 32 * j + lrow] =
+                    alpha * acc[i][j][r];
+        __syncthreads();
+        // RP rows x 64 values; a lane moves 8 consecutive values of a row
+#pragma unroll
+        for (int rr = 0; rr < RP / 8; ++rr) {
+            const uint32_t row = rr * 8 + (lane >> 3), c8 = (lane & 7) * 8;
+            const float *src = ep + row * EP_PITCH + c8;
+            const phx_f4 v0 = *(const phx_f4 *)src, v1 = *(const phx_f4 *)(src + 4);
+            TOut *dst = C + (int64_t)(m0 + wm + pass * RP + row) * ldc + n0 + wn + c8;
+#ifdef PHX_GEMM_TC
+            phx_f4 o0 = v0, o1 = v1;
+            if (beta != 0.0f) {
+                const phx_f4 c0 = *(const phx_f4 *)dst, c1 = *(const phx_f4 *)(dst + 4);
+                o0 = v0 + beta * c0;
+                o1 = v1 + beta * c1;
+            }
+            *(phx_f4 *)dst = o0;
+            *(phx_f4 *)(dst + 4) = o1;
+#else
+            float o[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+            if (beta != 0.0f) {
+                const phx_h8 c = *(const phx_h8 *)dst;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float cb = beta * (float)c[e];
+                    o[e] = o[e] + cb;
+                }
+            }
+            phx_h8 h;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) h[e] = (_Float16)o[e];
+            *(phx_h8 *)dst = h;
+#endif
+        }
+    }
+    __syncthreads();  // LDS is reused by the next tile
+}
+
+#ifndef PHX_GEMM_TC
+// ------------------------------------------------------------------ f16 path
+// f16 inputs go global -> LDS directly (buffer_load ... lds: lane l of a
+// 64-lane load writes LDS bytes base + 16l .. +15 from its own global
+// address, so the XOR-swizzled layouts are built by choosing each lane's
+// source).  Three 24 KiB stages, each its own LDS array so the compiler's
+// LDS-DMA tracking tells them apart; K step t+2 is in flight while step t
+// computes.  A wave waits for its own copies of a stage (vmcnt) before the
+// barrier that publishes it; the raw s_barrier carries no memory fence, so
+// nothing waits for the younger copies still in flight.
+#define DMA_PER_STEP 6  // buffer_load ... lds per wave per K step (4 A + 2 B)
+
+typedef __attribute__((address_space(3))) void *phx_lds_vp;
+
+// s_waitcnt with only vmcnt = n (expcnt and lgkmcnt left at their maxima)
+#define PHX_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14))
+
+// Copies K step kt of A and B into stage `dst` (per-lane offsets voa/vob,
+// wave w's share of the stage).
+__device__ __forceinline__ void dma_step(char *dst, const TIn *A, int64_t lda, const TIn *B,
+                                         int64_t ldb, uint32_t m0, uint32_t n0, uint32_t k0,
+                                         uint32_t voa, uint32_t vob, uint32_t wave) {
+    const __amdgpu_buffer_rsrc_t ra =
+        phx_rsrc(A + (int64_t)m0 * lda + k0, (uint32_t)((BM - 1) * lda + BK) * 2);
+    const __amdgpu_buffer_rsrc_t rb =
+        phx_rsrc(B + (int64_t)k0 * ldb + n0, (uint32_t)((BK - 1) * ldb + BN) * 2);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)  // A chunks wave*256 + i*64 + lane
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            ra, (phx_lds_vp)(dst + (wave * 256 + i * 64) * 16), 16, voa,
+            (int)((uint32_t)((wave * 64 + i * 16) * lda) * 2), 0, 0);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)  // B chunks wave*128 + i*64 + lane
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rb, (phx_lds_vp)(dst + A_BYTES + (wave * 128 + i * 64) * 16), 16, vob,
+            (int)((uint32_t)((wave * 8 + i * 4) * ldb) * 2), 0, 0);
+}
+
+// One K step on stage `cur`; issues the copy of step kt+2 into `fill`.
+__device__ __forceinline__ void dma_k_step(phx_f16v (&acc)[4][2], const char *cur, char *fill,
+                                           const TIn *A, int64_t lda, const TIn *B, int64_t ldb,
+                                           uint32_t m0, uint32_t n0, uint32_t kt, uint32_t nk,
+                                           uint32_t voa, uint32_t vob, uint32_t wm, uint32_t wn,
+                                           uint32_t wave, uint32_t lane) {
+    if (kt + 1 < nk)
+        PHX_WAIT_VMCNT(DMA_PER_STEP);  // own copies of step kt landed (kt+1 may fly)
+    else
+        PHX_WAIT_VMCNT(0);
+    __builtin_amdgcn_s_barrier();  // everyone's step kt visible; step kt-1 reads done
+    if (kt + 2 < nk) dma_step(fill, A, lda, B, ldb, m0, n0, (kt + 2) * BK, voa, vob, wave);
+    Frags f0, f1;
+    read_frags(f0, cur, 0, wm, wn, lane);
+    read_frags(f1, cur, 1, wm, wn, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_slice(acc, f0);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_slice(acc, f1);
+    __builtin_amdgcn_sched_barrier(0);
+}
+#endif
+
 extern "C" __global__ __launch_bounds__(NT, 2) void gemm(PHX_MEMREF2(TIn, a, int64_t),
                                                           PHX_MEMREF2(TIn, b, int64_t),
                                                           PHX_MEMREF2(TOut, c, int64_t),
                                                           float alpha, float beta) {
+#ifdef PHX_GEMM_TC
     __shared__ __attribute__((aligned(16))) char lds[2][STAGE_BYTES];
+#else
+    __shared__ __attribute__((aligned(16))) char stg0[STAGE_BYTES];
+    __shared__ __attribute__((aligned(16))) char stg1[STAGE_BYTES];
+    __shared__ __attribute__((aligned(16))) char stg2[STAGE_BYTES];
+#endif
 
     const int64_t M = a_s0, K = a_s1, N = b_s1;
     // Uniform preconditions (validated on the host by phx_check_shape; a
@@ -236,10 +365,18 @@ extern "C" __global__ __launch_bounds__(NT, 2) void gemm(PHX_MEMREF2(TIn, a, int
     const uint32_t ntiles = tiles_m * tiles_n;
     const uint32_t nblk = phx_block_count();
     const uint32_t nk = (uint32_t)(K / BK);
-    const uint32_t lrow = lane & 31, lgrp = lane >> 5;
+#ifdef PHX_GEMM_TC
     // per-lane byte offsets of the staging loads (see Stage)
     const uint32_t voa = (uint32_t)(((tid >> 2) * lda + (tid & 3) * 8) * sizeof(TIn));
     const uint32_t vob = (uint32_t)(((tid >> 4) * ldb + (tid & 15) * 8) * sizeof(TIn));
+#else
+    // per-lane byte offsets of the LDS copies (see dma_step): the chunk a
+    // lane fetches is the logical chunk its swizzled LDS slot holds.
+    const uint32_t voa =
+        (uint32_t)(((lane >> 2) * lda + 8 * ((lane & 3) ^ ((lane >> 4) & 3))) * 2);
+    const uint32_t vob =
+        (uint32_t)(((lane >> 4) * ldb + 8 * ((lane & 15) ^ (4 * ((lane >> 4) & 3)))) * 2);
+#endif
 
     for (uint32_t t = phx_block_linear(); t < ntiles; t += nblk) {
         const uint32_t ts = nblk == ntiles ? phx_xcd_swizzle(t, ntiles) : t;
@@ -257,6 +394,7 @@ extern "C" __global__ __launch_bounds__(NT, 2) void gemm(PHX_MEMREF2(TIn, a, int
             for (int j = 0; j < 2; ++j)
                 acc[i][j] = (phx_f16v){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 
+#ifdef PHX_GEMM_TC
         Stage st;
         load_stage(st, A, lda, B, ldb, m0, n0, 0, voa, vob);
         store_stage(st, lds[0], tid);
@@ -276,57 +414,25 @@ extern "C" __global__ __launch_bounds__(NT, 2) void gemm(PHX_MEMREF2(TIn, a, int
             if (kt + 1 < nk) store_stage(st, lds[(kt + 1) & 1], tid);
             __syncthreads();
         }
-
-        // Epilogue, staged through LDS so every global access is a 16-byte
-        // row chunk: in pass i each wave parks alpha*acc of its rows
-        // wm+32i .. +31 (32 x 64 floats, row pitch 68 floats so the two lane
-        // halves hit different banks), then reads it back row-wise.
-        // acc[i][j][r] sits at row 8*(r/4) + 4*lgrp + r%4, col 32j + lrow.
-        float *ep = (float *)(&lds[0][0]) + wave * (32 * EP_PITCH);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            __syncthreads();  // the previous pass (or the main loop) is done with LDS
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-#pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    ep[(8 * (r >> 2) + 4 * lgrp + (r & 3)) * EP_PITCH + 32 * j + lrow] =
-                        alpha * acc[i][j][r];
-            __syncthreads();
-            // 32 rows x 64 values; a lane moves 8 consecutive values of a row
-            // (8 lanes per row, 8 rows per round, 4 rounds)
-#pragma unroll
-            for (int rr = 0; rr < 4; ++rr) {
-                const uint32_t row = rr * 8 + (lane >> 3), c8 = (lane & 7) * 8;
-                const float *src = ep + row * EP_PITCH + c8;
-                const phx_f4 v0 = *(const phx_f4 *)src, v1 = *(const phx_f4 *)(src + 4);
-                TOut *dst = C + (int64_t)(m0 + wm + 32 * i + row) * ldc + n0 + wn + c8;
-#ifdef PHX_GEMM_TC
-                phx_f4 o0 = v0, o1 = v1;
-                if (beta != 0.0f) {
-                    const phx_f4 c0 = *(const phx_f4 *)dst, c1 = *(const phx_f4 *)(dst + 4);
-                    o0 = v0 + beta * c0;
-                    o1 = v1 + beta * c1;
-                }
-                *(phx_f4 *)dst = o0;
-                *(phx_f4 *)(dst + 4) = o1;
+        epilogue<32>(acc, (float *)&lds[0][0], C, ldc, m0, n0, wm, wn, alpha, beta, wave, lane);
 #else
-                float o[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-                if (beta != 0.0f) {
-                    const phx_h8 c = *(const phx_h8 *)dst;
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const float cb = beta * (float)c[e];
-                        o[e] = o[e] + cb;
-                    }
-                }
-                phx_h8 h;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) h[e] = (_Float16)o[e];
-                *(phx_h8 *)dst = h;
-#endif
-            }
+        dma_step(stg0, A, lda, B, ldb, m0, n0, 0, voa, vob, wave);
+        if (nk > 1) dma_step(stg1, A, lda, B, ldb, m0, n0, BK, voa, vob, wave);
+        uint32_t kt = 0;
+        for (; kt + 2 < nk; kt += 3) {
+            dma_k_step(acc, stg0, stg2, A, lda, B, ldb, m0, n0, kt, nk, voa, vob, wm, wn, wave, lane);
+            dma_k_step(acc, stg1, stg0, A, lda, B, ldb, m0, n0, kt + 1, nk, voa, vob, wm, wn, wave,
+                       lane);
+            dma_k_step(acc, stg2, stg1, A, lda, B, ldb, m0, n0, kt + 2, nk, voa, vob, wm, wn, wave,
+                       lane);
         }
-        __syncthreads();  // LDS is reused by the next tile's staging
+        if (kt < nk)
+            dma_k_step(acc, stg0, stg2, A, lda, B, ldb, m0, n0, kt, nk, voa, vob, wm, wn, wave, lane);
+        if (kt + 1 < nk)
+            dma_k_step(acc, stg1, stg0, A, lda, B, ldb, m0, n0, kt + 1, nk, voa, vob, wm, wn, wave,
+                       lane);
+        PHX_WAIT_VMCNT(0);
+        epilogue<16>(acc, (float *)stg0, C, ldc, m0, n0, wm, wn, alpha, beta, wave, lane);
+#endif
     }
 }
