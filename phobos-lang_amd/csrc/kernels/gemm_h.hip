@@ -19,30 +19,31 @@
 // differs from the reference only in the sign of an exactly-zero result.
 //
 // MI355X design
-//   * 256x128 output tile, K step 32, 256 threads = 4 waves (2x2) of 128x64,
-//     each 4x2 v_mfma_f32_32x32x16_f16 tiles (128 f32 accumulators).  LDS is
-//     72 KiB (f16) / 48 KiB (tc) and a wave stays under 256 registers, so two
-//     workgroups share each CU and cover each other's barrier, LDS and load stalls
-//     (at 4096^2: 512 tiles, two per CU, all resident at once).
-//   * A is staged As[m][k] (64-byte rows); an MFMA A operand (8 consecutive k
-//     of one row) is one ds_read_b128.  B stays row-major Bs[k][n] (256-byte
-//     rows) and its operand is read with gfx950's transposing
-//     ds_read_b64_tr_b16: in a 16-lane group, lane s supplies 4 halves of row
-//     k0 + s/4 at column n0 + 4*(s%4), and lane i receives B[k0..k0+3][n0+i].
-//     Two such reads give a lane its 8 consecutive k.  Staging is therefore a
-//     plain 16-byte copy for both operands.
+//   * 256x256 output tile per workgroup, one workgroup per CU (at 4096^2: 256
+//     tiles, one wave of workgroups).  4 waves in a 2x2 arrangement, each
+//     owning 128x128 = 4x4 v_mfma_f32_32x32x16_f16 tiles whose 256 f32
+//     accumulators live in AGPRs.  Per K slice of 16 a wave reads 8 KiB of
+//     operands from LDS for 16 MFMAs, half the LDS traffic per flop of a
+//     128x64 wave tile.
+//   * K step 32.  A is staged As[m][k] (64-byte rows); an MFMA A operand (8
+//     consecutive k of one row) is one ds_read_b128.  B stays row-major
+//     Bs[k][n] (512-byte rows) and its operand is read with gfx950's
+//     transposing ds_read_b64_tr_b16: in a 16-lane group, lane s supplies 4
+//     halves of row k0 + s/4 at column n0 + 4*(s%4), and lane i receives
+//     B[k0..k0+3][n0+i].  Two such reads give a lane its 8 consecutive k.
+//     Staging is therefore a plain 16-byte copy for both operands.
 //   * gfx950's LDS serves 64 banks (256 bytes) per clock.  The 16-byte chunk
 //     index is XOR-swizzled so every 16-lane (b128) or 32-lane (b64) group
 //     hits distinct banks: As chunk ^ ((row >> 2) & 3), Bs chunk ^ 4*(row % 4).
-//   * f16 inputs are copied global -> LDS directly (buffer_load ... lds, no
-//     VGPR staging) into a ring of three 24 KiB stages: K step t+2 is in
-//     flight while step t computes; each wave waits for its own copies
-//     (vmcnt) before the raw barrier that publishes a stage.  The tc variant
-//     (f32 inputs, converted to f16 on the way) stages through registers with
-//     a double-buffered LDS.  Both issue a K slice's LDS reads ahead of its
-//     MFMAs (fenced, since the wave issues in order).
-//   * Workgroups are renumbered XCD-major and grouped 8 tile-rows deep, so the
-//     64 workgroups of one XCD cover an 8x8 block of tiles and share A/B
+//   * Software pipeline, one barrier per K step: the MFMAs of slice 0 run
+//     while the slice-1 operands are read; then each wave waits for its own
+//     copies of the next step and for its reads, and passes the barrier; the
+//     MFMAs of slice 1 run while the next step's slice-0 operands are read and
+//     the copy of a later step is issued into the stage just released.
+//     Fences (sched_barrier / sched_group_barrier) fix the interleave, so the
+//     single wave per SIMD keeps its matrix pipe fed.
+//   * Workgroups are renumbered XCD-major and grouped 4 tile-rows deep, so the
+//     32 workgroups of one XCD cover a 4x8 block of tiles and share A/B
 //     panels in that XCD's L2.
 #include "phx_common.h"
 
@@ -55,22 +56,34 @@ typedef _Float16 TOut;
 #endif
 
 #define BM PHX_H_BM  // 256
-#define BN PHX_H_BN  // 128
+#define BN PHX_H_BN  // 256
 #define BK PHX_H_BK  // 32
 #define NT PHX_H_THREADS
-#define WM 128  // wave tile rows
-#define WN 64   // wave tile cols
-#define GROUP_M 8
+#define WM 128
+#define WN 128
+#define GROUP_M 4   // tile rows per swizzle group
 
 #define A_ROW_BYTES (BK * 2)             // 64
-#define B_ROW_BYTES (BN * 2)             // 256
+#define B_ROW_BYTES (BN * 2)             // 512
 #define A_BYTES (BM * A_ROW_BYTES)       // 16 KiB
-#define B_BYTES (BK * B_ROW_BYTES)       // 8 KiB
-#define STAGE_BYTES (A_BYTES + B_BYTES)  // 24 KiB
-#define EP_PITCH 68                      // epilogue LDS row pitch (floats)
+#define B_BYTES (BK * B_ROW_BYTES)       // 16 KiB
+#define STAGE_BYTES (A_BYTES + B_BYTES)  // 32 KiB
+#define EP_RP 8                         // epilogue rows per pass
+#define EP_PITCH 136                     // epilogue LDS row pitch (floats)
 
 typedef __fp16 phx_fp16x4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
 typedef __attribute__((address_space(3))) phx_fp16x4 *phx_lds_h4p;
+typedef __attribute__((address_space(3))) void *phx_lds_vp;
+
+// s_waitcnt fields: vmcnt [3:0]+[15:14], expcnt [6:4], lgkmcnt [11:8]
+#define PHX_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14))
+#define PHX_WAIT_VM_LGKM0(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (((n) >> 4) << 14))
+#define SGB(mask, n) __builtin_amdgcn_sched_group_barrier(mask, n, 0)
+#define G_MFMA 0x008
+#define G_VALU 0x002
+#define G_VMEM 0x020
+#define G_DSR 0x100
+#define G_DSW 0x200
 
 __device__ __forceinline__ uint32_t a_off(uint32_t row, uint32_t chunk) {
     return row * A_ROW_BYTES + ((chunk ^ ((row >> 2) & 3)) << 4);
@@ -79,103 +92,16 @@ __device__ __forceinline__ uint32_t b_off(uint32_t row, uint32_t chunk) {
     return row * B_ROW_BYTES + ((chunk ^ ((row & 3) << 2)) << 4);
 }
 
-// Buffer resource over `bytes` bytes from p (gfx9 dword3 = 0x00020000).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t phx_rsrc(const void *p, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes,
                                              0x00020000);
 }
 
-template <typename V>
-__device__ __forceinline__ V buf_load(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
-}
-
-// Global loads of one K step.  Thread t stages
-//   A: rows i*64 + t/4 (i < 4), 16-byte chunk t%4 (8 k values);
-//   B: rows t/16 and t/16 + 16, chunk t%16 (8 n values).
-struct Stage {
-#ifdef PHX_GEMM_TC
-    phx_f4 a[4][2];
-    phx_f4 b[2][2];
-#else
-    phx_u4 a[4];
-    phx_u4 b[2];
-#endif
-};
-
-__device__ __forceinline__ void load_stage(Stage &st, const TIn *A, int64_t lda, const TIn *B,
-                                           int64_t ldb, uint32_t m0, uint32_t n0, uint32_t k0,
-                                           uint32_t voa, uint32_t vob) {
-    const uint32_t esz = sizeof(TIn);
-    const __amdgpu_buffer_rsrc_t ra =
-        phx_rsrc(A + (int64_t)m0 * lda + k0, (uint32_t)((BM - 1) * lda + BK) * esz);
-    const __amdgpu_buffer_rsrc_t rb =
-        phx_rsrc(B + (int64_t)k0 * ldb + n0, (uint32_t)((BK - 1) * ldb + BN) * esz);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t so = (uint32_t)(i * 64 * lda) * esz;
-#ifdef PHX_GEMM_TC
-        st.a[i][0] = buf_load<phx_f4>(ra, voa, so);
-        st.a[i][1] = buf_load<phx_f4>(ra, voa + 16, so);
-#else
-        st.a[i] = buf_load<phx_u4>(ra, voa, so);
-#endif
-    }
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const uint32_t so = (uint32_t)(i * 16 * ldb) * esz;
-#ifdef PHX_GEMM_TC
-        st.b[i][0] = buf_load<phx_f4>(rb, vob, so);
-        st.b[i][1] = buf_load<phx_f4>(rb, vob + 16, so);
-#else
-        st.b[i] = buf_load<phx_u4>(rb, vob, so);
-#endif
-    }
-}
-
-#ifdef PHX_GEMM_TC
-__device__ __forceinline__ phx_u4 to_h8(const phx_f4 &lo, const phx_f4 &hi) {
-    phx_u4 v;
-    v.x = phx_pack_h2(lo.x, lo.y);
-    v.y = phx_pack_h2(lo.z, lo.w);
-    v.z = phx_pack_h2(hi.x, hi.y);
-    v.w = phx_pack_h2(hi.z, hi.w);
-    return v;
-}
-#endif
-
-__device__ __forceinline__ void store_stage(const Stage &st, char *stage, uint32_t tid) {
-    char *As = stage, *Bs = stage + A_BYTES;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#ifdef PHX_GEMM_TC
-        const phx_u4 v = to_h8(st.a[i][0], st.a[i][1]);
-#else
-        const phx_u4 v = st.a[i];
-#endif
-        *(phx_u4 *)(As + a_off(i * 64 + (tid >> 2), tid & 3)) = v;
-    }
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-#ifdef PHX_GEMM_TC
-        const phx_u4 v = to_h8(st.b[i][0], st.b[i][1]);
-#else
-        const phx_u4 v = st.b[i];
-#endif
-        *(phx_u4 *)(Bs + b_off(i * 16 + (tid >> 4), tid & 15)) = v;
-    }
-}
-
 struct Frags {
     phx_h8 a[4];
-    phx_h8 b[2];
+    phx_h8 b[4];
 };
 
-// Operands of K slice s (k = 16s .. 16s+15) for this wave.
-//   A: lane l reads row wm + 32i + l%32, k = 16s + 8*(l/32) .. +7.
-//   B: lane l needs column wn + 32j + l%32 at the same 8 k; two transposing
-//      reads (k +0..3, +4..7) from the lane's 16-lane group q = l/16, which
-//      covers columns 16*(q%2) .. +15 and k half q/2.
 __device__ __forceinline__ void read_frags(Frags &f, const char *stage, uint32_t s, uint32_t wm,
                                            uint32_t wn, uint32_t lane) {
     const char *As = stage;
@@ -186,8 +112,8 @@ __device__ __forceinline__ void read_frags(Frags &f, const char *stage, uint32_t
         f.a[i] = *(const phx_h8 *)(As + a_off(wm + i * 32 + lrow, 2 * s + g));
     const uint32_t q = lane >> 4, sl = lane & 15;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const uint32_t col = wn + j * 32 + 16 * (q & 1) + 4 * (sl & 3);  // halves
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t col = wn + j * 32 + 16 * (q & 1) + 4 * (sl & 3);
         phx_fp16x4 h[2];
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
@@ -202,150 +128,278 @@ __device__ __forceinline__ void read_frags(Frags &f, const char *stage, uint32_t
     }
 }
 
-__device__ __forceinline__ void mfma_slice(phx_f16v (&acc)[4][2], const Frags &f) {
+__device__ __forceinline__ void mfma_all(phx_f16v (&acc)[4][4], const Frags &f) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < 4; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
 }
 
-// Epilogue, staged through LDS so every global access is a 16-byte row
-// chunk: each pass parks alpha*acc for RP rows of every wave's tile in `ep`
-// (row pitch EP_PITCH floats, so the two lane halves hit different banks) and
-// reads it back row-wise.  acc[i][j][r] sits at tile row 32i + 8*(r/4) +
-// 4*lgrp + r%4, column 32j + lrow.  Uses 4 * RP * EP_PITCH * 4 bytes of LDS.
-template <int RP>
-__device__ __forceinline__ void epilogue(const phx_f16v (&acc)[4][2], float *ep_all, TOut *C,
+// Epilogue: per wave, 8 passes of 16 rows x 128 columns through a private
+// LDS region; a lane then moves 4 consecutive values of a row.
+__device__ __forceinline__ void epilogue(const phx_f16v (&acc)[4][4], float *ep_all, TOut *C,
                                          int64_t ldc, uint32_t m0, uint32_t n0, uint32_t wm,
                                          uint32_t wn, float alpha, float beta, uint32_t wave,
                                          uint32_t lane) {
     const uint32_t lrow = lane & 31, lgrp = lane >> 5;
-    float *ep = ep_all + wave * (RP * EP_PITCH);
+    float *ep = ep_all + wave * (EP_RP * EP_PITCH);
 #pragma unroll
-    for (int pass = 0; pass < WM / RP; ++pass) {
-        __syncthreads();  // the previous pass (or the main loop) is done with LDS
-        const int i = (pass * RP) / 32;
-        const int r0 = ((pass * RP) % 32) / 2;  // first accumulator register of this pass
+    for (int pass = 0; pass < WM / EP_RP; ++pass) {
+        const int i = (pass * EP_RP) / 32;
+        const int r0 = ((pass * EP_RP) % 32) / 2;  // first accumulator register of this pass
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
-            for (int r = r0; r < r0 + RP / 2; ++r)
+            for (int r = r0; r < r0 + EP_RP / 2; ++r)
                 ep[(8 * (r >> 2) + 4 * lgrp + (r & 3) - 2 * r0) * EP_PITCH + 32 * j + lrow] =
                     alpha * acc[i][j][r];
-        __syncthreads();
-        // RP rows x 64 values; a lane moves 8 consecutive values of a row
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-        for (int rr = 0; rr < RP / 8; ++rr) {
-            const uint32_t row = rr * 8 + (lane >> 3), c8 = (lane & 7) * 8;
-            const float *src = ep + row * EP_PITCH + c8;
-            const phx_f4 v0 = *(const phx_f4 *)src, v1 = *(const phx_f4 *)(src + 4);
-            TOut *dst = C + (int64_t)(m0 + wm + pass * RP + row) * ldc + n0 + wn + c8;
+        for (int rr = 0; rr < EP_RP / 2; ++rr) {
+            const uint32_t row = rr * 2 + (lane >> 5), c4 = (lane & 31) * 4;
+            const phx_f4 v = *(const phx_f4 *)(ep + row * EP_PITCH + c4);
+            TOut *dst = C + (int64_t)(m0 + wm + pass * EP_RP + row) * ldc + n0 + wn + c4;
 #ifdef PHX_GEMM_TC
-            phx_f4 o0 = v0, o1 = v1;
+            phx_f4 o = v;
             if (beta != 0.0f) {
-                const phx_f4 c0 = *(const phx_f4 *)dst, c1 = *(const phx_f4 *)(dst + 4);
-                o0 = v0 + beta * c0;
-                o1 = v1 + beta * c1;
+                const phx_f4 c = *(const phx_f4 *)dst;
+                o = v + beta * c;
             }
-            *(phx_f4 *)dst = o0;
-            *(phx_f4 *)(dst + 4) = o1;
+            *(phx_f4 *)dst = o;
 #else
-            float o[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+            float o[4] = {v.x, v.y, v.z, v.w};
             if (beta != 0.0f) {
-                const phx_h8 c = *(const phx_h8 *)dst;
+                const phx_h4 c = *(const phx_h4 *)dst;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
+                for (int e = 0; e < 4; ++e) {
                     const float cb = beta * (float)c[e];
                     o[e] = o[e] + cb;
                 }
             }
-            phx_h8 h;
+            phx_h4 h;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) h[e] = (_Float16)o[e];
-            *(phx_h8 *)dst = h;
+            for (int e = 0; e < 4; ++e) h[e] = (_Float16)o[e];
+            *(phx_h4 *)dst = h;
 #endif
         }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
-    __syncthreads();  // LDS is reused by the next tile
 }
 
-#ifndef PHX_GEMM_TC
+#ifdef PHX_GEMM_TC
+// ------------------------------------------------------------------ tc path
+// f32 inputs are staged through registers and rounded to f16 (RNE) on the
+// way into LDS.  Thread t stages f16 chunks c = i*256 + t (i < 4) of A (row
+// c/4, chunk c%4) and of B (row c/32, chunk c%32); each chunk is two 16-byte
+// f32 loads.
+#define ESZ 4u
+struct Chunk { phx_f4 lo, hi; };
+__device__ __forceinline__ Chunk load_chunk(__amdgpu_buffer_rsrc_t r, uint32_t vo, int so) {
+    Chunk c;
+    c.lo = __builtin_bit_cast(phx_f4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)vo, so, 0));
+    c.hi = __builtin_bit_cast(phx_f4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)vo + 16, so, 0));
+    return c;
+}
+__device__ __forceinline__ phx_u4 pack(const Chunk &c) {
+    phx_u4 v;
+    v.x = phx_pack_h2(c.lo.x, c.lo.y);
+    v.y = phx_pack_h2(c.lo.z, c.lo.w);
+    v.z = phx_pack_h2(c.hi.x, c.hi.y);
+    v.w = phx_pack_h2(c.hi.z, c.hi.w);
+    return v;
+}
+struct Regs {
+    Chunk a[4];
+    Chunk b[4];
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t a_rsrc(const TIn *A, int64_t lda, int64_t K,
+                                                         uint32_t m0, uint32_t k0) {
+    const bool in = (int64_t)k0 < K;
+    return phx_rsrc(A + (int64_t)m0 * lda + (in ? k0 : 0), in ? (uint32_t)((BM - 1) * lda + BK) * ESZ : 0);
+}
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t b_rsrc(const TIn *B, int64_t ldb, int64_t K,
+                                                         uint32_t n0, uint32_t k0) {
+    const bool in = (int64_t)k0 < K;
+    return phx_rsrc(B + (int64_t)(in ? k0 : 0) * ldb + n0, in ? (uint32_t)((BK - 1) * ldb + BN) * ESZ : 0);
+}
+
+__device__ __forceinline__ void load_regs(Regs &R, const TIn *A, int64_t lda, const TIn *B,
+                                          int64_t ldb, int64_t K, uint32_t m0, uint32_t n0,
+                                          uint32_t k0, uint32_t voa, uint32_t vob) {
+    const __amdgpu_buffer_rsrc_t ra = a_rsrc(A, lda, K, m0, k0);
+    const __amdgpu_buffer_rsrc_t rb = b_rsrc(B, ldb, K, n0, k0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) R.a[i] = load_chunk(ra, voa, (int)((uint32_t)(i * 64 * lda) * ESZ));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) R.b[i] = load_chunk(rb, vob, (int)((uint32_t)(i * 8 * ldb) * ESZ));
+}
+
+__device__ __forceinline__ void store_regs(const Regs &R, char *stage, uint32_t tid) {
+    char *As = stage, *Bs = stage + A_BYTES;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *(phx_u4 *)(As + a_off(i * 64 + (tid >> 2), tid & 3)) = pack(R.a[i]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *(phx_u4 *)(Bs + b_off(i * 8 + (tid >> 5), tid & 31)) = pack(R.b[i]);
+}
+
+__device__ __forceinline__ void mfma_one(phx_f16v (&acc)[4][4], const Frags &f, int m) {
+    acc[m >> 2][m & 3] =
+        __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[m >> 2], f.b[m & 3], acc[m >> 2][m & 3], 0, 0, 0);
+}
+
+__device__ __forceinline__ void read_a(Frags &f, const char *stage, uint32_t s, uint32_t wm,
+                                       uint32_t lane, int i) {
+    f.a[i] = *(const phx_h8 *)(stage + a_off(wm + i * 32 + (lane & 31), 2 * s + (lane >> 5)));
+}
+
+__device__ __forceinline__ void read_b(Frags &f, const char *stage, uint32_t s, uint32_t wn,
+                                       uint32_t lane, int j) {
+    const char *Bs = stage + A_BYTES;
+    const uint32_t q = lane >> 4, sl = lane & 15;
+    const uint32_t col = wn + j * 32 + 16 * (q & 1) + 4 * (sl & 3);
+    phx_fp16x4 h[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const uint32_t row = 16 * s + 8 * (q >> 1) + 4 * t + (sl >> 2);
+        const uint32_t off = b_off(row, col >> 3) + ((col & 7) << 1);
+        h[t] = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+            (phx_lds_h4p)((__attribute__((address_space(3))) char *)(Bs + off)));
+    }
+    phx_h4 lo = __builtin_bit_cast(phx_h4, h[0]);
+    phx_h4 hi = __builtin_bit_cast(phx_h4, h[1]);
+    f.b[j] = (phx_h8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// One K step on LDS stage `cur`.  R holds step kt+2 (converted into `cur`
+// once every wave is done reading it) and is then refilled with step kt+4.
+// The second half is hand-interleaved: each MFMA is followed by one piece of
+// the other work, so the matrix pipe never waits behind a long VALU/LDS run.
+__device__ __forceinline__ void tc_step(phx_f16v (&acc)[4][4], Frags &F0, Frags &F1, char *cur,
+                                        const char *nxt, Regs &R, const TIn *A, int64_t lda,
+                                        const TIn *B, int64_t ldb, int64_t K, uint32_t m0,
+                                        uint32_t n0, uint32_t kt, uint32_t voa, uint32_t vob,
+                                        uint32_t wm, uint32_t wn, uint32_t tid, uint32_t lane) {
+    read_frags(F1, cur, 1, wm, wn, lane);
+    mfma_all(acc, F0);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        SGB(G_MFMA, 1);
+        if (i < 12) SGB(G_DSR, 1);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    PHX_WAIT_VM_LGKM0(63);  // reads of cur and earlier LDS writes done
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+
+    const uint32_t k4 = (kt + 4) * BK;
+    const __amdgpu_buffer_rsrc_t ra = a_rsrc(A, lda, K, m0, k4);
+    const __amdgpu_buffer_rsrc_t rb = b_rsrc(B, ldb, K, n0, k4);
+    char *As = cur, *Bs = cur + A_BYTES;
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+        mfma_one(acc, F1, m);
+        if (m < 4) {
+            read_a(F0, nxt, 0, wm, lane, m);
+        } else if (m < 8) {
+            read_b(F0, nxt, 0, wn, lane, m - 4);
+        } else if (m < 12) {
+            const int i = m - 8;
+            *(phx_u4 *)(As + a_off(i * 64 + (tid >> 2), tid & 3)) = pack(R.a[i]);
+            R.a[i] = load_chunk(ra, voa, (int)((uint32_t)(i * 64 * lda) * ESZ));
+        } else {
+            const int i = m - 12;
+            *(phx_u4 *)(Bs + b_off(i * 8 + (tid >> 5), tid & 31)) = pack(R.b[i]);
+            R.b[i] = load_chunk(rb, vob, (int)((uint32_t)(i * 8 * ldb) * ESZ));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+#else
 // ------------------------------------------------------------------ f16 path
 // f16 inputs go global -> LDS directly (buffer_load ... lds: lane l of a
-// 64-lane load writes LDS bytes base + 16l .. +15 from its own global
+// 64-lane copy writes LDS bytes base + 16l .. +15 from its own global
 // address, so the XOR-swizzled layouts are built by choosing each lane's
-// source).  Three 24 KiB stages, each its own LDS array so the compiler's
-// LDS-DMA tracking tells them apart; K step t+2 is in flight while step t
-// computes.  A wave waits for its own copies of a stage (vmcnt) before the
-// barrier that publishes it; the raw s_barrier carries no memory fence, so
-// nothing waits for the younger copies still in flight.
-#define DMA_PER_STEP 6  // buffer_load ... lds per wave per K step (4 A + 2 B)
+// source) into a ring of NSTG stages, each its own LDS array so the
+// compiler's LDS-DMA tracking tells them apart.  Step t+NSTG is copied into
+// the stage step t used, once every wave is past the barrier that ends its
+// reads.  Copies of K steps past the end read through an empty buffer
+// resource (zeros) into stages nobody reads, which keeps every wait count
+// constant.
+#define DMA_PER_STEP 8  // copies per wave per K step (4 A + 4 B)
+#define NSTG 3
 
-typedef __attribute__((address_space(3))) void *phx_lds_vp;
-
-// s_waitcnt with only vmcnt = n (expcnt and lgkmcnt left at their maxima)
-#define PHX_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14))
-
-// Copies K step kt of A and B into stage `dst` (per-lane offsets voa/vob,
-// wave w's share of the stage).
 __device__ __forceinline__ void dma_step(char *dst, const TIn *A, int64_t lda, const TIn *B,
-                                         int64_t ldb, uint32_t m0, uint32_t n0, uint32_t k0,
-                                         uint32_t voa, uint32_t vob, uint32_t wave) {
+                                         int64_t ldb, int64_t K, uint32_t m0, uint32_t n0,
+                                         uint32_t k0, uint32_t voa, uint32_t vob0, uint32_t vob1,
+                                         uint32_t wave) {
+    const bool in = (int64_t)k0 < K;
     const __amdgpu_buffer_rsrc_t ra =
-        phx_rsrc(A + (int64_t)m0 * lda + k0, (uint32_t)((BM - 1) * lda + BK) * 2);
+        phx_rsrc(A + (int64_t)m0 * lda + (in ? k0 : 0), in ? (uint32_t)((BM - 1) * lda + BK) * 2 : 0);
     const __amdgpu_buffer_rsrc_t rb =
-        phx_rsrc(B + (int64_t)k0 * ldb + n0, (uint32_t)((BK - 1) * ldb + BN) * 2);
+        phx_rsrc(B + (int64_t)(in ? k0 : 0) * ldb + n0, in ? (uint32_t)((BK - 1) * ldb + BN) * 2 : 0);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)  // A chunks wave*256 + i*64 + lane
+    for (int i = 0; i < 4; ++i)  // A chunks wave*256 + i*64 + lane: row wave*64 + i*16 + lane/4
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             ra, (phx_lds_vp)(dst + (wave * 256 + i * 64) * 16), 16, voa,
             (int)((uint32_t)((wave * 64 + i * 16) * lda) * 2), 0, 0);
 #pragma unroll
-    for (int i = 0; i < 2; ++i)  // B chunks wave*128 + i*64 + lane
+    for (int i = 0; i < 4; ++i)  // B chunks wave*256 + i*64 + lane: row wave*8 + 2i + lane/32
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rb, (phx_lds_vp)(dst + A_BYTES + (wave * 128 + i * 64) * 16), 16, vob,
-            (int)((uint32_t)((wave * 8 + i * 4) * ldb) * 2), 0, 0);
+            rb, (phx_lds_vp)(dst + A_BYTES + (wave * 256 + i * 64) * 16), 16, (i & 1) ? vob1 : vob0,
+            (int)((uint32_t)((wave * 8 + i * 2) * ldb) * 2), 0, 0);
 }
 
-// One K step on stage `cur`; issues the copy of step kt+2 into `fill`.
-__device__ __forceinline__ void dma_k_step(phx_f16v (&acc)[4][2], const char *cur, char *fill,
-                                           const TIn *A, int64_t lda, const TIn *B, int64_t ldb,
-                                           uint32_t m0, uint32_t n0, uint32_t kt, uint32_t nk,
-                                           uint32_t voa, uint32_t vob, uint32_t wm, uint32_t wn,
-                                           uint32_t wave, uint32_t lane) {
-    if (kt + 1 < nk)
-        PHX_WAIT_VMCNT(DMA_PER_STEP);  // own copies of step kt landed (kt+1 may fly)
-    else
-        PHX_WAIT_VMCNT(0);
-    __builtin_amdgcn_s_barrier();  // everyone's step kt visible; step kt-1 reads done
-    if (kt + 2 < nk) dma_step(fill, A, lda, B, ldb, m0, n0, (kt + 2) * BK, voa, vob, wave);
-    Frags f0, f1;
-    read_frags(f0, cur, 0, wm, wn, lane);
-    read_frags(f1, cur, 1, wm, wn, lane);
+__device__ __forceinline__ void dma_k_step(phx_f16v (&acc)[4][4], Frags &F0, Frags &F1, char *cur,
+                                           const char *nxt, const TIn *A, int64_t lda,
+                                           const TIn *B, int64_t ldb, int64_t K, uint32_t m0,
+                                           uint32_t n0, uint32_t kt, uint32_t voa, uint32_t vob0,
+                                           uint32_t vob1, uint32_t wm, uint32_t wn, uint32_t wave,
+                                           uint32_t lane) {
+    read_frags(F1, cur, 1, wm, wn, lane);
+    mfma_all(acc, F0);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        SGB(G_MFMA, 1);
+        if (i < 12) SGB(G_DSR, 1);
+    }
     __builtin_amdgcn_sched_barrier(0);
-    mfma_slice(acc, f0);
+    PHX_WAIT_VM_LGKM0((NSTG - 2) * DMA_PER_STEP);  // own copies of kt+1 landed, reads of cur done
+    __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    mfma_slice(acc, f1);
+    read_frags(F0, nxt, 0, wm, wn, lane);
+    dma_step(cur, A, lda, B, ldb, K, m0, n0, (kt + NSTG) * BK, voa, vob0, vob1, wave);
+    mfma_all(acc, F1);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        SGB(G_MFMA, 1);
+        if (i < 12) SGB(G_DSR, 1);
+        if (i < 8) SGB(G_VMEM, 1);
+    }
     __builtin_amdgcn_sched_barrier(0);
 }
 #endif
 
-extern "C" __global__ __launch_bounds__(NT, 2) void gemm(PHX_MEMREF2(TIn, a, int64_t),
+extern "C" __global__ __launch_bounds__(NT, 1) void gemm(PHX_MEMREF2(TIn, a, int64_t),
                                                           PHX_MEMREF2(TIn, b, int64_t),
                                                           PHX_MEMREF2(TOut, c, int64_t),
                                                           float alpha, float beta) {
 #ifdef PHX_GEMM_TC
-    __shared__ __attribute__((aligned(16))) char lds[2][STAGE_BYTES];
+    __shared__ __attribute__((aligned(16))) char stg0[STAGE_BYTES];
+    __shared__ __attribute__((aligned(16))) char stg1[STAGE_BYTES];
 #else
     __shared__ __attribute__((aligned(16))) char stg0[STAGE_BYTES];
     __shared__ __attribute__((aligned(16))) char stg1[STAGE_BYTES];
     __shared__ __attribute__((aligned(16))) char stg2[STAGE_BYTES];
+    char *const S[NSTG] = {stg0, stg1, stg2};
 #endif
 
     const int64_t M = a_s0, K = a_s1, N = b_s1;
-    // Uniform preconditions (validated on the host by phx_check_shape; a
-    // launch that breaks them writes nothing).
     if (blockDim.x != NT || M % BM || N % BN || K % BK || M <= 0 || N <= 0 || K <= 0 ||
         b_s0 != K || c_s0 != M || c_s1 != N || a_st1 != 1 || b_st1 != 1 || c_st1 != 1)
         return;
@@ -357,7 +411,7 @@ extern "C" __global__ __launch_bounds__(NT, 2) void gemm(PHX_MEMREF2(TIn, a, int
 
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63;
-    const uint32_t wave = tid >> 6;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t wm = (wave >> 1) * WM;
     const uint32_t wn = (wave & 1) * WN;
     const uint32_t tiles_n = (uint32_t)(N / BN);
@@ -366,16 +420,16 @@ extern "C" __global__ __launch_bounds__(NT, 2) void gemm(PHX_MEMREF2(TIn, a, int
     const uint32_t nblk = phx_block_count();
     const uint32_t nk = (uint32_t)(K / BK);
 #ifdef PHX_GEMM_TC
-    // per-lane byte offsets of the staging loads (see Stage)
-    const uint32_t voa = (uint32_t)(((tid >> 2) * lda + (tid & 3) * 8) * sizeof(TIn));
-    const uint32_t vob = (uint32_t)(((tid >> 4) * ldb + (tid & 15) * 8) * sizeof(TIn));
+    const uint32_t voa = (uint32_t)(((tid >> 2) * lda + (tid & 3) * 8) * ESZ);
+    const uint32_t vob = (uint32_t)(((tid >> 5) * ldb + (tid & 31) * 8) * ESZ);
 #else
-    // per-lane byte offsets of the LDS copies (see dma_step): the chunk a
-    // lane fetches is the logical chunk its swizzled LDS slot holds.
     const uint32_t voa =
         (uint32_t)(((lane >> 2) * lda + 8 * ((lane & 3) ^ ((lane >> 4) & 3))) * 2);
-    const uint32_t vob =
-        (uint32_t)(((lane >> 4) * ldb + 8 * ((lane & 15) ^ (4 * ((lane >> 4) & 3)))) * 2);
+    // B row parity within the 4-row swizzle period: 2*(i&1) + lane/32
+    const uint32_t vob0 =
+        (uint32_t)(((lane >> 5) * ldb + 8 * ((lane & 31) ^ (4 * (lane >> 5)))) * 2);
+    const uint32_t vob1 =
+        (uint32_t)(((lane >> 5) * ldb + 8 * ((lane & 31) ^ (4 * (2 + (lane >> 5))))) * 2);
 #endif
 
     for (uint32_t t = phx_block_linear(); t < ntiles; t += nblk) {
@@ -387,52 +441,63 @@ extern "C" __global__ __launch_bounds__(NT, 2) void gemm(PHX_MEMREF2(TIn, a, int
         const uint32_t tn = (ts % gsz) / gm;
         const uint32_t m0 = tm * BM, n0 = tn * BN;
 
-        phx_f16v acc[4][2];
+        phx_f16v acc[4][4];
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
+            for (int j = 0; j < 4; ++j)
                 acc[i][j] = (phx_f16v){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+        Frags F0, F1;
 
 #ifdef PHX_GEMM_TC
-        Stage st;
-        load_stage(st, A, lda, B, ldb, m0, n0, 0, voa, vob);
-        store_stage(st, lds[0], tid);
-        __syncthreads();
-
-        for (uint32_t kt = 0; kt < nk; ++kt) {
-            const char *cur = lds[kt & 1];
-            Frags f0, f1;
-            read_frags(f0, cur, 0, wm, wn, lane);
-            if (kt + 1 < nk) load_stage(st, A, lda, B, ldb, m0, n0, (kt + 1) * BK, voa, vob);
-            read_frags(f1, cur, 1, wm, wn, lane);
-            __builtin_amdgcn_sched_barrier(0);
-            mfma_slice(acc, f0);
-            __builtin_amdgcn_sched_barrier(0);
-            mfma_slice(acc, f1);
-            __builtin_amdgcn_sched_barrier(0);
-            if (kt + 1 < nk) store_stage(st, lds[(kt + 1) & 1], tid);
-            __syncthreads();
-        }
-        epilogue<32>(acc, (float *)&lds[0][0], C, ldc, m0, n0, wm, wn, alpha, beta, wave, lane);
-#else
-        dma_step(stg0, A, lda, B, ldb, m0, n0, 0, voa, vob, wave);
-        if (nk > 1) dma_step(stg1, A, lda, B, ldb, m0, n0, BK, voa, vob, wave);
+        // prologue: steps 0 and 1 into LDS, steps 2 and 3 in flight
+        Regs R0, R1;
+        load_regs(R0, A, lda, B, ldb, K, m0, n0, 0, voa, vob);
+        load_regs(R1, A, lda, B, ldb, K, m0, n0, BK, voa, vob);
+        store_regs(R0, stg0, tid);
+        store_regs(R1, stg1, tid);
+        load_regs(R0, A, lda, B, ldb, K, m0, n0, 2 * BK, voa, vob);
+        load_regs(R1, A, lda, B, ldb, K, m0, n0, 3 * BK, voa, vob);
+        PHX_WAIT_VM_LGKM0(63);
+        __builtin_amdgcn_s_barrier();
+        read_frags(F0, stg0, 0, wm, wn, lane);
         uint32_t kt = 0;
-        for (; kt + 2 < nk; kt += 3) {
-            dma_k_step(acc, stg0, stg2, A, lda, B, ldb, m0, n0, kt, nk, voa, vob, wm, wn, wave, lane);
-            dma_k_step(acc, stg1, stg0, A, lda, B, ldb, m0, n0, kt + 1, nk, voa, vob, wm, wn, wave,
-                       lane);
-            dma_k_step(acc, stg2, stg1, A, lda, B, ldb, m0, n0, kt + 2, nk, voa, vob, wm, wn, wave,
-                       lane);
+        for (; kt + 1 < nk; kt += 2) {
+            tc_step(acc, F0, F1, stg0, stg1, R0, A, lda, B, ldb, K, m0, n0, kt, voa, vob, wm, wn,
+                    tid, lane);
+            tc_step(acc, F0, F1, stg1, stg0, R1, A, lda, B, ldb, K, m0, n0, kt + 1, voa, vob, wm,
+                    wn, tid, lane);
         }
         if (kt < nk)
-            dma_k_step(acc, stg0, stg2, A, lda, B, ldb, m0, n0, kt, nk, voa, vob, wm, wn, wave, lane);
-        if (kt + 1 < nk)
-            dma_k_step(acc, stg1, stg0, A, lda, B, ldb, m0, n0, kt + 1, nk, voa, vob, wm, wn, wave,
-                       lane);
+            tc_step(acc, F0, F1, stg0, stg1, R0, A, lda, B, ldb, K, m0, n0, kt, voa, vob, wm, wn,
+                    tid, lane);
         PHX_WAIT_VMCNT(0);
-        epilogue<16>(acc, (float *)stg0, C, ldc, m0, n0, wm, wn, alpha, beta, wave, lane);
+        __syncthreads();
+        epilogue(acc, (float *)stg0, C, ldc, m0, n0, wm, wn, alpha, beta, wave, lane);
+        __syncthreads();
+#else
+#pragma unroll
+        for (int p = 0; p < NSTG; ++p)  // prologue: steps 0 .. NSTG-1 in flight
+            dma_step(S[p], A, lda, B, ldb, K, m0, n0, p * BK, voa, vob0, vob1, wave);
+        PHX_WAIT_VMCNT((NSTG - 1) * DMA_PER_STEP);
+        __builtin_amdgcn_s_barrier();
+        read_frags(F0, stg0, 0, wm, wn, lane);
+        uint32_t kt = 0;
+        for (; kt + NSTG <= nk; kt += NSTG) {
+#pragma unroll
+            for (int u = 0; u < NSTG; ++u)
+                dma_k_step(acc, F0, F1, S[u], S[(u + 1) % NSTG], A, lda, B, ldb, K, m0, n0, kt + u,
+                           voa, vob0, vob1, wm, wn, wave, lane);
+        }
+#pragma unroll
+        for (int u = 0; u < NSTG - 1; ++u)
+            if (kt + u < nk)
+                dma_k_step(acc, F0, F1, S[u], S[(u + 1) % NSTG], A, lda, B, ldb, K, m0, n0, kt + u,
+                           voa, vob0, vob1, wm, wn, wave, lane);
+        PHX_WAIT_VMCNT(0);
+        __syncthreads();
+        epilogue(acc, (float *)stg0, C, ldc, m0, n0, wm, wn, alpha, beta, wave, lane);
+        __syncthreads();
 #endif
     }
 }

@@ -14,10 +14,10 @@
 #endif
 #define PHX_SAXPY_BLOCK_ELEMS (PHX_SAXPY_THREADS * PHX_SAXPY_VEC * 4)
 
-// f16-operand GEMMs (gemm_fp16, gemm_fp16tc_fp32acc): 256x128 output tile,
-// K step 32, 256 threads = 4 waves in a 2x2 arrangement of 128x64.
+// f16-operand GEMMs (gemm_fp16, gemm_fp16tc_fp32acc): 256x256 output tile,
+// K step 32, 256 threads = 4 waves in a 2x2 arrangement of 128x128.
 #define PHX_H_BM 256
-#define PHX_H_BN 128
+#define PHX_H_BN 256
 #define PHX_H_BK 32
 #define PHX_H_THREADS 256
 

@@ -62,7 +62,7 @@ def test_grid_for_and_shape_checks():
     g, b = px.grid_for(px.SAXPY_FP32, [1 << 24])
     assert b == (256, 1, 1) and g == ((1 << 24) // 4096, 1, 1)
     g, b = px.grid_for(px.GEMM_FP16TC_FP32ACC, [4096, 4096, 4096])
-    assert g == (512, 1, 1) and b == (256, 1, 1)
+    assert g == (256, 1, 1) and b == (256, 1, 1)
     g, b = px.grid_for(px.GEMM_FP32, [4096, 4096, 4096])
     assert g == (1024, 1, 1)
     g, b = px.grid_for(px.FLASH_FP16_BH, [64, 4096, 4096, 64])

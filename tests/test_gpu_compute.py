@@ -87,3 +87,32 @@ def test_gemm_rejects_bad_shapes(px_gpu, stream):
     assert e.value.code == px.PHX_E_INVALID
     with pytest.raises(px.PhxError):
         px.launch_flash(stream, px.FLASH_FP16, 0, 0, 0, 0, 100, 4096, 64, 0.125)
+
+
+@pytest.mark.parametrize("kernel,grid", [("GEMM_FP16", 2), ("GEMM_FP16TC_FP32ACC", 4),
+                                         ("GEMM_FP16", 17), ("GEMM_FP16TC_FP32ACC", 9)])
+def test_f16_gemms_any_grid(px_gpu, stream, kernel, grid):
+    # The reference derives the GEMM grid from its own tile sizes
+    # (main.rs:500-508); these kernels walk their tiles block-stride, so a grid
+    # smaller than the tile count (several tiles per workgroup, LDS reused
+    # across tiles) or larger (idle workgroups) gives the same result.
+    px = px_gpu
+    k = getattr(px, kernel)
+    f16 = kernel == "GEMM_FP16"
+    M, N, K = 768, 512, 96   # 6 output tiles of 256x256
+    A = oracle.f16_round(oracle.normal_f32(11, M * K, 1 / np.sqrt(K)))
+    B = oracle.f16_round(oracle.normal_f32(12, K * N, 1 / np.sqrt(K)))
+    if f16:
+        dA, dB = px.DeviceBuffer.from_array(oracle.f16_bits(A)), px.DeviceBuffer.from_array(oracle.f16_bits(B))
+        dC, dR = px.DeviceBuffer(M * N * 2), px.DeviceBuffer(M * N * 2)
+    else:
+        dA, dB = px.DeviceBuffer.from_array(A), px.DeviceBuffer.from_array(B)
+        dC, dR = px.DeviceBuffer(M * N * 4), px.DeviceBuffer(M * N * 4)
+    px.launch_gemm(stream, k, dA.ptr, dB.ptr, dR.ptr, M, N, K, 1.0, 0.0)
+    fn = px.builtin_function(k)
+    px.compute(fn, 64, [(dA.ptr, (M, K)), (dB.ptr, (K, N)), (dC.ptr, (M, N))],
+               [(3, 4, px.f32_bits(1.0)), (4, 4, px.f32_bits(0.0))], (grid, 1, 1), (256, 1, 1),
+               stream)
+    stream.synchronize()
+    dt = np.uint16 if f16 else np.uint32
+    assert np.array_equal(dC.download(dt, M * N), dR.download(dt, M * N))

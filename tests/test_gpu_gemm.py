@@ -90,7 +90,10 @@ def test_gemm_integer_fixture_exact(px_gpu, stream):
     assert np.array_equal(got[:96, :100], oracle.f16_round(want))
 
 
-@pytest.mark.parametrize("M,N,K", [(256, 256, 64), (512, 768, 320), (256, 512, 2048)])
+# K = 32 and 96 are one and three K steps (the pipelines' tail paths), 320 is
+# ten; 768 columns are three tile columns.
+@pytest.mark.parametrize("M,N,K", [(256, 256, 32), (256, 256, 64), (256, 512, 96), (512, 768, 320),
+                                   (256, 512, 2048)])
 def test_gemm_fp16tc_full_small(px_gpu, stream, M, N, K):
     A = oracle.f16_round(oracle.normal_f32(1, M * K, 1 / np.sqrt(K))).reshape(M, K)
     B = oracle.f16_round(oracle.normal_f32(2, K * N, 1 / np.sqrt(K))).reshape(K, N)
@@ -115,7 +118,8 @@ def test_gemm_fp16tc_rounds_f32_inputs_to_f16(px_gpu, stream):
     assert e16 < 1e-3 and e16 < e32 / 10
 
 
-@pytest.mark.parametrize("M,N,K", [(256, 256, 64), (512, 256, 1024)])
+@pytest.mark.parametrize("M,N,K", [(256, 256, 32), (256, 256, 64), (512, 256, 96), (768, 512, 160),
+                                   (512, 256, 1024)])
 def test_gemm_fp16_full_small(px_gpu, stream, M, N, K):
     A = oracle.normal_f32(3, M * K, 1 / np.sqrt(K)).reshape(M, K)
     B = oracle.normal_f32(4, K * N, 1 / np.sqrt(K)).reshape(K, N)
