@@ -54,9 +54,8 @@ typedef float T;
 #define ROW_BYTES (D * 4)  // 256 bytes
 #endif
 #define TILE_BYTES (BC * ROW_BYTES)  // BC == D == 64 rows
-// two workgroups (8 waves) per CU for the f16 path
 #ifdef PHX_FLASH_F16
-#define FA_MIN_BLOCKS 2
+#define FA_MIN_BLOCKS 2  // two workgroups per CU
 #else
 #define FA_MIN_BLOCKS 1
 #endif
@@ -77,235 +76,285 @@ __device__ __forceinline__ float shfl_xor32(float v) { return __shfl_xor(v, 32, 
 
 #ifdef PHX_FLASH_F16
 // ---------------------------------------------------------------- f16 path
-// K and V are both staged as plain 16-byte row copies (K by threads 128-255,
-// V by threads 0-127, 4 buffer loads each).  K runs one block ahead of V:
-// during block j the LDS holds K_{j+1} (for the next scores) and V_j.
-struct Stage {
-    phx_u4 r[4];
-};
+// 256 queries per workgroup: 4 waves x 64 queries (two 32-query halves h),
+// two workgroups per CU (a wave stays under 256 registers), so each SIMD runs
+// two waves whose softmax (VALU) and matrix work (MFMA) overlap.  Per 64-key
+// block a wave runs 32 MFMAs (S^T for both halves: 16; O^T += V^T.P^T for
+// both halves: 16) on 16 KiB of K/V operands read from LDS, half the LDS
+// traffic per flop of a 32-query wave; each run of MFMAs rotates over four
+// independent accumulators.
+//
+// K and V blocks are copied global -> LDS directly (buffer_load ... lds, 16
+// bytes per lane) into a ring of 4 stages (K 8 KiB + V 8 KiB each): block
+// i+3 is issued when block i starts, and one barrier per block publishes it.
+#define WQ 64                  // queries per wave
+#define QB (4 * WQ)            // queries per workgroup
+#define KV_ROW 128             // bytes per K or V row (64 f16)
+#define KV_TILE (BC * KV_ROW)  // 8 KiB
+#define STAGE_BYTES (2 * KV_TILE)
+#define NSTAGE 4
+#define DMA_PER_BLK 4          // copies per wave per key block (2 K + 2 V)
 
 typedef __fp16 phx_fp16x4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
 typedef __attribute__((address_space(3))) phx_fp16x4 *phx_lds_h4p;
+typedef __attribute__((address_space(3))) void *phx_lds_vp;
+
+#define PHX_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14))
+#define PHX_WAIT_VM_LGKM0(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (((n) >> 4) << 14))
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t phx_rsrc(const void *p, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes,
                                              0x00020000);
 }
 
-// V rows (128 bytes) are read with ds_read_b64_tr_b16: a 32-lane service
-// group touches 4 consecutive rows x 64 bytes, so rows 2 apart are shifted by
-// 64 bytes to land on distinct banks.
+// K rows are read as b128 MFMA operands (16 lanes = 16 rows, one chunk):
+// XOR the chunk with (row>>1)&7.  V rows are read with ds_read_b64_tr_b16 (a
+// 32-lane group touches 4 consecutive rows x 64 bytes): rows 2 apart are
+// shifted by 64 bytes.
+__device__ __forceinline__ uint32_t k_off(uint32_t row, uint32_t chunk) {
+    return row * KV_ROW + ((chunk ^ ((row >> 1) & 7)) << 4);
+}
 __device__ __forceinline__ uint32_t v_off(uint32_t row, uint32_t chunk) {
-    return row * ROW_BYTES + ((chunk ^ (((row >> 1) & 1) << 2)) << 4);
+    return row * KV_ROW + ((chunk ^ (((row >> 1) & 1) << 2)) << 4);
 }
 
-// Thread u of a 128-thread half stages rows i*16 + u/8 (i < 4), chunk u%8.
-__device__ __forceinline__ void load_stage(Stage &st, __amdgpu_buffer_rsrc_t r, uint32_t rowb,
-                                           uint32_t blk, bool val, uint32_t vo) {
-    if (!val) return;
+// Copies key block blk (K and V rows wave*16 .. +15) into stage dst.  Lane l
+// of copy i lands at LDS row wave*16 + 8i + l/8, physical chunk l%8; its
+// source is the logical chunk stored there.  Blocks past the end read an
+// empty buffer (zeros) into a stage that is never consumed.
+__device__ __forceinline__ void dma_block(char *dst, const T *Kp, const T *Vp, int64_t ldk,
+                                          int64_t ldv, uint32_t Nk, uint32_t blk, uint32_t vk0,
+                                          uint32_t vk1, uint32_t vv, uint32_t wave) {
+    const bool in = blk * BC < Nk;
+    const uint32_t r0 = in ? blk * BC : 0;
+    const __amdgpu_buffer_rsrc_t rk =
+        phx_rsrc(Kp + (int64_t)r0 * ldk, in ? (uint32_t)(((BC - 1) * ldk + D) * 2) : 0);
+    const __amdgpu_buffer_rsrc_t rv =
+        phx_rsrc(Vp + (int64_t)r0 * ldv, in ? (uint32_t)(((BC - 1) * ldv + D) * 2) : 0);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-        st.r[i] = __builtin_bit_cast(
-            phx_u4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)(vo + i * 16 * rowb),
-                                                          (int)(blk * BC * rowb), 0));
+    for (int i = 0; i < 2; ++i)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rk, (phx_lds_vp)(dst + (wave * 16 + i * 8) * KV_ROW), 16, i ? vk1 : vk0,
+            (int)((uint32_t)((wave * 16 + i * 8) * ldk) * 2), 0, 0);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rv, (phx_lds_vp)(dst + KV_TILE + (wave * 16 + i * 8) * KV_ROW), 16, vv,
+            (int)((uint32_t)((wave * 16 + i * 8) * ldv) * 2), 0, 0);
 }
 
-__device__ __forceinline__ void store_stage(const Stage &st, char *Ks, char *Vs, bool kval,
-                                            bool vval, uint32_t tid) {
-    const uint32_t u = tid & 127, ch = u & 7;
-    if (tid < 128) {
-        if (!vval) return;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            *(phx_u4 *)(Vs + v_off(i * 16 + (u >> 3), ch)) = st.r[i];
-    } else {
-        if (!kval) return;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            *(phx_u4 *)(Ks + lds_off(i * 16 + (u >> 3), ch)) = st.r[i];
-    }
-}
-
-// S^T = K . Q^T for one key block: sT[t] holds keys 32t + 8(r/4) + 4g + r%4
-// of query lq.
-__device__ __forceinline__ void scores(phx_f16v (&sT)[2], const char *Ks, const phx_h8 (&qf)[4],
-                                       uint32_t lq, uint32_t g) {
-    phx_h8 kf[2][4];
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-            kf[t][s] = *(const phx_h8 *)(Ks + lds_off(32 * t + lq, 2 * s + g));
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        sT[t] = (phx_f16v){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-            sT[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[t][s], qf[s], sT[t], 0, 0, 0);
-    }
-}
-
-// The running max is raised only when a row's block max exceeds it by more
-// than RESCALE_SLACK (in log2 units), so the O/l rescale is skipped on almost
-// every block; p = exp2(s*c - m) then stays <= 2^8, which f16 P and f32 l
-// hold as well as the reference's per-block update.  O = acc / l is the same
-// quantity either way.
+// RESCALE_SLACK: the running max is raised only when a row's block max
+// exceeds it by more than 8 (log2 units), so the O/l rescale is skipped on
+// almost every block; p = exp2(s*c - m) then stays <= 2^8, which f16 P and
+// f32 l hold as well as the reference's per-block update.  O = acc / l is
+// the same quantity either way.
 #define RESCALE_SLACK 8.0f
 
-struct FlashState {
-    phx_f16v acc[2];
-    float m2, l;
+struct Flash16 {
+    phx_f16v acc[2][2];  // [half][d tile]: d = 32dt + 8(r/4) + 4g + r%4, query lq
+    float m2[2], l[2];
+    phx_h8 qf[2][4];     // Q^T operand, half h, d slice s: d = 16s + 8g .. +7
 };
 
-// One key block: issue the next block's scores (K_{kb+1}, MFMA pipe), then
-// this block's softmax (VALU) and P.V (V_kb); stage K_{kb+2} / V_{kb+1}.
-__device__ __forceinline__ void flash_step(FlashState &fs, phx_f16v (&sT)[2], phx_f16v (&sN)[2],
-                                           Stage &st, char (*lds)[2][TILE_BYTES],
-                                           const phx_h8 (&qf)[4], __amdgpu_buffer_rsrc_t rk,
-                                           __amdgpu_buffer_rsrc_t rv, uint32_t kbr, uint32_t vbr,
-                                           uint32_t vo, uint32_t kb, uint32_t nkb, float c2,
-                                           uint32_t tid, uint32_t lane) {
-    const uint32_t lq = lane & 31, g = lane >> 5;
-    const uint32_t cur = kb & 1, nxt = cur ^ 1;
-    const bool more = kb + 1 < nkb;
-    if (tid < 128)
-        load_stage(st, rv, vbr, kb + 1, more, vo);
-    else
-        load_stage(st, rk, kbr, kb + 2, kb + 2 < nkb, vo);
-    if (more) scores(sN, lds[nxt][0], qf, lq, g);
-    __builtin_amdgcn_sched_barrier(0);
-
-    float mx = sT[0][0];
-#pragma unroll
-    for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sT[0][r]);
-#pragma unroll
-    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sT[1][r]);
-    mx = fmaxf(mx, shfl_xor32(mx)) * c2;
-    if (__ballot(mx > fs.m2 + RESCALE_SLACK)) {  // wave-uniform
-        const float m2new = fmaxf(fs.m2, mx);
-        const float corr = __builtin_amdgcn_exp2f(fs.m2 - m2new);
-        fs.l = fs.l * corr;
-        fs.acc[0] = fs.acc[0] * corr;
-        fs.acc[1] = fs.acc[1] * corr;
-        fs.m2 = m2new;
-    }
-    // P (f16) and its row sum: v_dot2_f32_f16 against (1, 1) adds the two
-    // f16 values of a pair into an f32 sum.
-    const phx_h2 ones = {(_Float16)1.0f, (_Float16)1.0f};
-    float ps = 0.0f;
-    phx_h8 pf[4];
+// S^T for both halves: s[h][t] holds keys 32t + 8(r/4) + 4g + r%4 of query
+// 32h + lq.  K operands kf[t][s] = K row 32t + lq, d 16s + 8g .. +7.
+__device__ __forceinline__ void read_k(phx_h8 (&kf)[2][4], const char *Ks, uint32_t lq,
+                                       uint32_t g) {
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-            phx_h8 v;
-#pragma unroll
-            for (int j = 0; j < 8; j += 2) {
-                const float p0 =
-                    __builtin_amdgcn_exp2f(__builtin_fmaf(sT[t][8 * hh + j], c2, -fs.m2));
-                const float p1 =
-                    __builtin_amdgcn_exp2f(__builtin_fmaf(sT[t][8 * hh + j + 1], c2, -fs.m2));
-                const phx_h2 pp = {(_Float16)p0, (_Float16)p1};
-                ps = __builtin_amdgcn_fdot2(pp, ones, ps, false);
-                v[j] = pp.x;
-                v[j + 1] = pp.y;
-            }
-            pf[2 * t + hh] = v;
-        }
-    ps += shfl_xor32(ps);
-    fs.l = fs.l + ps;
-
-    // O^T[dt] += V^T[32 d rows, 16 keys of block c] . P^T.  The A operand
-    // of lane group g holds keys 16c + 4g + 0..3 and 16c + 8 + 4g + 0..3 (the
-    // order P's registers have), read as two transposing 4-key runs.
-    const char *Vs = lds[cur][1];
-    const uint32_t q = lane >> 4, sl = lane & 15;
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-#pragma unroll
-        for (int dt = 0; dt < 2; ++dt) {
-            const uint32_t col = 32 * dt + 16 * (q & 1) + 4 * (sl & 3);  // d
-            phx_fp16x4 h[2];
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                const uint32_t row = 16 * c + 8 * t + 4 * (q >> 1) + (sl >> 2);  // key
-                const uint32_t off = v_off(row, col >> 3) + ((col & 7) << 1);
-                h[t] = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-                    (phx_lds_h4p)((__attribute__((address_space(3))) char *)(Vs + off)));
-            }
-            const phx_h4 lo = __builtin_bit_cast(phx_h4, h[0]);
-            const phx_h4 hi = __builtin_bit_cast(phx_h4, h[1]);
-            const phx_h8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-            fs.acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[c], fs.acc[dt], 0, 0, 0);
-        }
-    // K_{kb+2} -> buffer cur (its K_kb fed the scores one block ago);
-    // V_{kb+1} -> buffer nxt (its V_{kb-1} is done).
-    store_stage(st, lds[cur][0], lds[nxt][1], kb + 2 < nkb, more, tid);
-    __syncthreads();
+        for (int s = 0; s < 4; ++s)
+            kf[t][s] = *(const phx_h8 *)(Ks + k_off(32 * t + lq, 2 * s + g));
 }
+
+// MFMA m of the 16: d slice s = m/4 outermost, so consecutive MFMAs update
+// four independent accumulators.
+__device__ __forceinline__ void mfma_s(phx_f16v (&sN)[2][2], const phx_h8 (&kf)[2][4],
+                                       const phx_h8 (&qf)[2][4], int m) {
+    const int s = m >> 2, h = (m >> 1) & 1, t = m & 1;
+    if (s == 0) sN[h][t] = (phx_f16v){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    sN[h][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[t][s], qf[h][s], sN[h][t], 0, 0, 0);
+}
+
+// V^T operand for keys 16c + (4g + 0..3, 8 + 4g + 0..3) (the order P's
+// registers have) and d rows 32dt + lane%32: two transposing 4-key reads.
+__device__ __forceinline__ phx_h8 read_v(const char *Vs, int c, int dt, uint32_t lane) {
+    const uint32_t q = lane >> 4, sl = lane & 15;
+    const uint32_t col = 32 * dt + 16 * (q & 1) + 4 * (sl & 3);  // d
+    phx_fp16x4 h[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const uint32_t row = 16 * c + 8 * t + 4 * (q >> 1) + (sl >> 2);  // key
+        const uint32_t off = v_off(row, col >> 3) + ((col & 7) << 1);
+        h[t] = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+            (phx_lds_h4p)((__attribute__((address_space(3))) char *)(Vs + off)));
+    }
+    const phx_h4 lo = __builtin_bit_cast(phx_h4, h[0]);
+    const phx_h4 hi = __builtin_bit_cast(phx_h4, h[1]);
+    return (phx_h8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// exp2(s*c2 - m2) of half h as f16 MFMA operands pf[c] (keys 16c + ...),
+// and the f32 row sum of the f16 values (v_dot2_f32_f16 against (1, 1)).
+__device__ __forceinline__ void softmax_p(phx_h8 (&pf)[4], float &ps, const phx_f16v (&s)[2],
+                                          float c2, float m2) {
+    const phx_h2 ones = {(_Float16)1.0f, (_Float16)1.0f};
+    float part[4];  // one partial sum per key slice: four short dependency chains
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        phx_h8 v;
+        part[c] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; j += 2) {
+            const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[c >> 1][8 * (c & 1) + j], c2, -m2));
+            const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[c >> 1][8 * (c & 1) + j + 1], c2, -m2));
+            const phx_h2 pp = {(_Float16)p0, (_Float16)p1};
+            part[c] = __builtin_amdgcn_fdot2(pp, ones, part[c], false);
+            v[j] = pp.x;
+            v[j + 1] = pp.y;
+        }
+        pf[c] = v;
+    }
+    ps = (part[0] + part[1]) + (part[2] + part[3]);
+}
+
+// max over a lane's 32 scores of one half (3-input max tree), then across
+// the two lane halves.
+__device__ __forceinline__ float row_max(const phx_f16v (&s)[2]) {
+    float m[11];
+#pragma unroll
+    for (int j = 0; j < 10; ++j) {
+        const int a = 3 * j, b = a + 1, c = a + 2;
+        m[j] = fmaxf(s[a >> 4][a & 15], fmaxf(s[b >> 4][b & 15], s[c >> 4][c & 15]));
+    }
+    m[10] = fmaxf(s[1][14], s[1][15]);
+    const float x = fmaxf(m[0], fmaxf(m[1], m[2])), y = fmaxf(m[3], fmaxf(m[4], m[5]));
+    const float z = fmaxf(m[6], fmaxf(m[7], m[8])), w = fmaxf(m[9], m[10]);
+    const float r = fmaxf(fmaxf(x, y), fmaxf(z, w));
+    return fmaxf(r, __shfl_xor(r, 32, 64));
+}
+
+// One key block i, in order: scores, row max and lazy rescale, P and its row
+// sums, P.V.  cur = stage of block i, fill = stage that receives block i+3.
+__device__ __forceinline__ void flash16_step(Flash16 &fs, const char *cur, char *fill,
+                                             const T *Kp, const T *Vp, int64_t ldk, int64_t ldv,
+                                             uint32_t Nk, uint32_t i, float c2, uint32_t vk0,
+                                             uint32_t vk1, uint32_t vv, uint32_t wave,
+                                             uint32_t lane) {
+    const uint32_t lq = lane & 31, g = lane >> 5;
+    PHX_WAIT_VM_LGKM0(2 * DMA_PER_BLK);  // own copies of block i landed
+    __builtin_amdgcn_s_barrier();          // everyone's block i landed, block i-1 done
+    __builtin_amdgcn_sched_barrier(0);
+    dma_block(fill, Kp, Vp, ldk, ldv, Nk, i + 3, vk0, vk1, vv, wave);
+    phx_f16v sc[2][2];
+    {
+        phx_h8 kf[2][4];
+        read_k(kf, cur, lq, g);
+#pragma unroll
+        for (int m = 0; m < 16; ++m) mfma_s(sc, kf, fs.qf, m);
+    }
+    phx_h8 pf[2][4];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const float mx = row_max(sc[h]) * c2;
+        if (__ballot(mx > fs.m2[h] + RESCALE_SLACK)) {  // wave-uniform
+            const float m2new = fmaxf(fs.m2[h], mx);
+            const float corr = __builtin_amdgcn_exp2f(fs.m2[h] - m2new);
+            fs.l[h] = fs.l[h] * corr;
+            fs.acc[h][0] = fs.acc[h][0] * corr;
+            fs.acc[h][1] = fs.acc[h][1] * corr;
+            fs.m2[h] = m2new;
+        }
+        float ps;
+        softmax_p(pf[h], ps, sc[h], c2, fs.m2[h]);
+        fs.l[h] += ps + __shfl_xor(ps, 32, 64);
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        phx_h8 vf[2];
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt) vf[dt] = read_v(cur + KV_TILE, c, dt, lane);
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int dt = 0; dt < 2; ++dt)
+                fs.acc[h][dt] =
+                    __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[dt], pf[h][c], fs.acc[h][dt], 0, 0, 0);
+    }
+}
+
 
 __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp, T *O,
                                             int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo,
-                                            uint32_t Nk, uint32_t q0, float scale,
-                                            char (*lds)[2][TILE_BYTES]) {
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+                                            uint32_t Nq, uint32_t Nk, uint32_t q0, float scale,
+                                            char *st0, char *st1, char *st2, char *st3) {
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t lq = lane & 31, g = lane >> 5;
-    const uint32_t myq = q0 + wave * 32 + lq;
+    const uint32_t qw = q0 + wave * WQ;  // first query of this wave
     const float c2 = scale * LOG2E;
     const uint32_t nkb = Nk / BC;
+    char *const S[NSTAGE] = {st0, st1, st2, st3};
 
-    // buffer views of this head's K and V; vo = this thread's staging offset
-    const uint32_t kbr = (uint32_t)(ldk * 2), vbr = (uint32_t)(ldv * 2);
-    const __amdgpu_buffer_rsrc_t rk = phx_rsrc(Kp, (uint32_t)((Nk - 1) * kbr + D * 2));
-    const __amdgpu_buffer_rsrc_t rv = phx_rsrc(Vp, (uint32_t)((Nk - 1) * vbr + D * 2));
-    const uint32_t u = tid & 127;
-    const uint32_t vo = (u >> 3) * (tid < 128 ? vbr : kbr) + 16 * (u & 7);
+    // per-lane source offsets of the LDS copies (see dma_block)
+    const uint32_t vk0 =
+        (uint32_t)(((lane >> 3) * ldk + 8 * ((lane & 7) ^ ((lane >> 4) & 3))) * 2);
+    const uint32_t vk1 =
+        (uint32_t)(((lane >> 3) * ldk + 8 * ((lane & 7) ^ (4 + ((lane >> 4) & 3)))) * 2);
+    const uint32_t vv =
+        (uint32_t)(((lane >> 3) * ldv + 8 * ((lane & 7) ^ (((lane >> 4) & 1) << 2))) * 2);
 
-    // Q^T operand: s-step s covers d = 16s + 8g .. +7
-    phx_h8 qf[4];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) qf[s] = *(const phx_h8 *)(Q + (int64_t)myq * ldq + 16 * s + 8 * g);
+    for (int p = 0; p < 3; ++p) dma_block(S[p], Kp, Vp, ldk, ldv, Nk, p, vk0, vk1, vv, wave);
 
-    FlashState fs;
-    fs.acc[0] = (phx_f16v){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-    fs.acc[1] = fs.acc[0];
-    fs.m2 = M_INIT * LOG2E;
-    fs.l = 0.0f;
-
-    // prologue: V_0 -> buffer 0 (threads 0-127), K_0 -> buffer 0 then K_1 ->
-    // buffer 1 (threads 128-255)
-    Stage st;
-    if (tid < 128) {
-        load_stage(st, rv, vbr, 0, true, vo);
-        store_stage(st, lds[0][0], lds[0][1], false, true, tid);
-    } else {
-        load_stage(st, rk, kbr, 0, true, vo);
-        store_stage(st, lds[0][0], lds[0][1], true, false, tid);
-        load_stage(st, rk, kbr, 1, nkb > 1, vo);
-        store_stage(st, lds[1][0], lds[1][1], nkb > 1, false, tid);
+    Flash16 fs;
+    // Q rows past Nq read as zeros (their outputs are not stored)
+    const __amdgpu_buffer_rsrc_t rq = phx_rsrc(Q, (uint32_t)(((Nq - 1) * ldq + D) * 2));
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+            fs.qf[h][s] = __builtin_bit_cast(
+                phx_h8, __builtin_amdgcn_raw_buffer_load_b128(
+                            rq, (int)(((qw + 32 * h + lq) * ldq + 16 * s + 8 * g) * 2), 0, 0));
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        fs.acc[h][0] = (phx_f16v){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+        fs.acc[h][1] = fs.acc[h][0];
+        fs.m2[h] = M_INIT * LOG2E;
+        fs.l[h] = 0.0f;
     }
+
+    uint32_t i = 0;
+    for (; i + NSTAGE <= nkb; i += NSTAGE) {
+        flash16_step(fs, S[0], S[3], Kp, Vp, ldk, ldv, Nk, i, c2, vk0, vk1, vv, wave, lane);
+        flash16_step(fs, S[1], S[0], Kp, Vp, ldk, ldv, Nk, i + 1, c2, vk0, vk1, vv, wave, lane);
+        flash16_step(fs, S[2], S[1], Kp, Vp, ldk, ldv, Nk, i + 2, c2, vk0, vk1, vv, wave, lane);
+        flash16_step(fs, S[3], S[2], Kp, Vp, ldk, ldv, Nk, i + 3, c2, vk0, vk1, vv, wave, lane);
+    }
+    if (i < nkb) flash16_step(fs, S[0], S[3], Kp, Vp, ldk, ldv, Nk, i, c2, vk0, vk1, vv, wave, lane);
+    if (i + 1 < nkb) flash16_step(fs, S[1], S[0], Kp, Vp, ldk, ldv, Nk, i + 1, c2, vk0, vk1, vv, wave, lane);
+    if (i + 2 < nkb) flash16_step(fs, S[2], S[1], Kp, Vp, ldk, ldv, Nk, i + 2, c2, vk0, vk1, vv, wave, lane);
+    // drain the copies of the blocks past the end before the LDS is reused
+    PHX_WAIT_VMCNT(0);
     __syncthreads();
 
-    phx_f16v s0[2], s1[2];
-    scores(s0, lds[0][0], qf, lq, g);
-    uint32_t kb = 0;
-    for (; kb + 1 < nkb; kb += 2) {
-        flash_step(fs, s0, s1, st, lds, qf, rk, rv, kbr, vbr, vo, kb, nkb, c2, tid, lane);
-        flash_step(fs, s1, s0, st, lds, qf, rk, rv, kbr, vbr, vo, kb + 1, nkb, c2, tid, lane);
+    // acc[h][dt][r]: d = 32dt + 8(r/4) + 4g + r%4, query qw + 32h + lq.
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const uint32_t q = qw + 32 * h + lq;
+        if (q >= Nq) continue;
+        T *orow = O + (int64_t)q * ldo;
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                phx_h4 v;
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) v[rr] = (_Float16)(fs.acc[h][dt][4 * b + rr] / fs.l[h]);
+                *(phx_h4 *)(orow + 32 * dt + 8 * b + 4 * g) = v;
+            }
     }
-    if (kb < nkb) flash_step(fs, s0, s1, st, lds, qf, rk, rv, kbr, vbr, vo, kb, nkb, c2, tid, lane);
-
-    // acc[dt][r]: d = 32dt + 8(r/4) + 4g + r%4, query lq.
-    T *orow = O + (int64_t)myq * ldo;
-#pragma unroll
-    for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            phx_h4 v;
-#pragma unroll
-            for (int rr = 0; rr < 4; ++rr) v[rr] = (_Float16)(fs.acc[dt][4 * b + rr] / fs.l);
-            *(phx_h4 *)(orow + 32 * dt + 8 * b + 4 * g) = v;
-        }
 }
 #else
 // ---------------------------------------------------------------- f32 path
@@ -460,21 +509,37 @@ __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp
 }
 #endif
 
+#ifdef PHX_FLASH_F16
+#define FA_QB QB  // queries per workgroup
+#define FA_LDS_DECL                                                   \
+    __shared__ __attribute__((aligned(16))) char st0[STAGE_BYTES]; \
+    __shared__ __attribute__((aligned(16))) char st1[STAGE_BYTES]; \
+    __shared__ __attribute__((aligned(16))) char st2[STAGE_BYTES]; \
+    __shared__ __attribute__((aligned(16))) char st3[STAGE_BYTES];
+#define FA_CALL(Qp, Kp, Vp, Op, ldq, ldk, ldv, ldo, Nq, Nk, q0) \
+    flash_block(Qp, Kp, Vp, Op, ldq, ldk, ldv, ldo, Nq, Nk, q0, scale, st0, st1, st2, st3)
+#else
+#define FA_QB BR
+#define FA_LDS_DECL __shared__ __attribute__((aligned(16))) char lds[2][2][TILE_BYTES];
+#define FA_CALL(Qp, Kp, Vp, Op, ldq, ldk, ldv, ldo, Nq, Nk, q0) \
+    flash_block(Qp, Kp, Vp, Op, ldq, ldk, ldv, ldo, Nk, q0, scale, lds)
+#endif
+
 extern "C" __global__ __launch_bounds__(NT, FA_MIN_BLOCKS) void flash_attention(PHX_MEMREF2(T, q, int64_t),
                                                                   PHX_MEMREF2(T, k, int64_t),
                                                                   PHX_MEMREF2(T, v, int64_t),
                                                                   PHX_MEMREF2(T, o, int64_t),
                                                                   float scale) {
-    __shared__ __attribute__((aligned(16))) char lds[2][2][TILE_BYTES];
+    FA_LDS_DECL
     const int64_t Nq = q_s0, Nk = k_s0;
     if (blockDim.x != NT || q_s1 != D || k_s1 != D || v_s1 != D || o_s1 != D || v_s0 != Nk ||
         o_s0 != Nq || Nq % BR || Nk % BC || Nq <= 0 || Nk <= 0 || q_st1 != 1 || k_st1 != 1 ||
         v_st1 != 1 || o_st1 != 1)
         return;
-    const uint32_t nrb = (uint32_t)(Nq / BR);
+    const uint32_t nrb = (uint32_t)((Nq + FA_QB - 1) / FA_QB);
     for (uint32_t rb = phx_block_linear(); rb < nrb; rb += phx_block_count())
-        flash_block(q_ptr + q_off, k_ptr + k_off, v_ptr + v_off, o_ptr + o_off, q_st0, k_st0,
-                    v_st0, o_st0, (uint32_t)Nk, rb * BR, scale, lds);
+        FA_CALL(q_ptr + q_off, k_ptr + k_off, v_ptr + v_off, o_ptr + o_off, q_st0, k_st0, v_st0,
+                o_st0, (uint32_t)Nq, (uint32_t)Nk, rb * FA_QB);
 }
 
 extern "C" __global__ __launch_bounds__(NT, FA_MIN_BLOCKS) void flash_attention_bh(PHX_MEMREF3(T, q, int64_t),
@@ -482,20 +547,20 @@ extern "C" __global__ __launch_bounds__(NT, FA_MIN_BLOCKS) void flash_attention_
                                                                      PHX_MEMREF3(T, v, int64_t),
                                                                      PHX_MEMREF3(T, o, int64_t),
                                                                      float scale) {
-    __shared__ __attribute__((aligned(16))) char lds[2][2][TILE_BYTES];
+    FA_LDS_DECL
     const int64_t H = q_s0, Nq = q_s1, Nk = k_s1;
     if (blockDim.x != NT || k_s0 != H || v_s0 != H || o_s0 != H || q_s2 != D || k_s2 != D ||
         v_s2 != D || o_s2 != D || v_s1 != Nk || o_s1 != Nq || Nq % BR || Nk % BC || Nq <= 0 ||
         Nk <= 0 || H <= 0 || q_st2 != 1 || k_st2 != 1 || v_st2 != 1 || o_st2 != 1)
         return;
-    const uint32_t nrb = (uint32_t)(Nq / BR);
+    const uint32_t nrb = (uint32_t)((Nq + FA_QB - 1) / FA_QB);
     const uint32_t nwork = nrb * (uint32_t)H;
     const uint32_t nblk = phx_block_count();
     for (uint32_t w = phx_block_linear(); w < nwork; w += nblk) {
         const uint32_t ws = nblk == nwork ? phx_xcd_swizzle(w, nwork) : w;
         const uint32_t h = ws / nrb, rb = ws % nrb;
-        flash_block(q_ptr + q_off + h * q_st0, k_ptr + k_off + h * k_st0,
-                    v_ptr + v_off + h * v_st0, o_ptr + o_off + h * o_st0, q_st1, k_st1, v_st1,
-                    o_st1, (uint32_t)Nk, rb * BR, scale, lds);
+        FA_CALL(q_ptr + q_off + h * q_st0, k_ptr + k_off + h * k_st0, v_ptr + v_off + h * v_st0,
+                o_ptr + o_off + h * o_st0, q_st1, k_st1, v_st1, o_st1, (uint32_t)Nq, (uint32_t)Nk,
+                rb * FA_QB);
     }
 }

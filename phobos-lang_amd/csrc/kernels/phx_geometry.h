@@ -32,8 +32,11 @@
 #define PHX_EW_THREADS 256
 #define PHX_EW_BLOCK_ELEMS (256 * 16)
 
-// flash attention: 128 query rows per block (4 waves x 32), 64 keys per step.
+// flash attention: Nq must be a multiple of PHX_FA_BR; 64 keys per step.
+// f32: 128 query rows per workgroup (4 waves x 32).  f16: 256 query rows per
+// workgroup (4 waves x 64; rows past Nq are computed but not stored).
 #define PHX_FA_BR 128
+#define PHX_FA16_BR 256
 #define PHX_FA_BC 64
 #define PHX_FA_THREADS 256
 #define PHX_FA_D 64

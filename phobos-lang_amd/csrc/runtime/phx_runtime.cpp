@@ -256,12 +256,17 @@ int grid_for(phx_kernel k, const int64_t *d, int nd, uint32_t grid[3], uint32_t 
         break;
     }
     case PHX_FLASH_FP32:
-    case PHX_FLASH_FP16:
         grid[0] = (uint32_t)(d[0] / PHX_FA_BR);
         break;
+    case PHX_FLASH_FP16:
+        grid[0] = (uint32_t)((d[0] + PHX_FA16_BR - 1) / PHX_FA16_BR);
+        break;
     case PHX_FLASH_FP32_BH:
-    case PHX_FLASH_FP16_BH:
         grid[0] = (uint32_t)(d[1] / PHX_FA_BR);
+        grid[1] = (uint32_t)d[0];
+        break;
+    case PHX_FLASH_FP16_BH:
+        grid[0] = (uint32_t)((d[1] + PHX_FA16_BR - 1) / PHX_FA16_BR);
         grid[1] = (uint32_t)d[0];
         break;
     default:

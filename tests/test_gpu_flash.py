@@ -41,7 +41,10 @@ def _inputs(shape, bits, seed0=1, scale=1.0):
 
 
 @pytest.mark.parametrize("bits", [16, 32])
-@pytest.mark.parametrize("Nq,Nk", [(128, 64), (128, 320), (384, 1024)])
+# Nk/64 = 1, 3, 5, 6, 7, 16 key blocks covers every tail of the 4-stage copy
+# ring; Nq = 128, 384, 640 leaves the last 256-row f16 workgroup half full.
+@pytest.mark.parametrize("Nq,Nk", [(128, 64), (256, 192), (128, 320), (128, 384), (640, 448),
+                                   (384, 1024)])
 def test_flash_one_head_full(px_gpu, stream, bits, Nq, Nk):
     D = 64
     q, _, _ = _inputs((Nq, D), bits, 1)
@@ -120,3 +123,39 @@ def test_flash_baseline_config_sampled(px_gpu, stream, bits):
         want = oracle.flash_rows(rows, q[h], k[h], v[h], 0.125)
         worst = max(worst, _rel(got[h][rows.astype(int)], want))
     assert worst < TOL[bits], worst
+
+
+def test_flash16_rows_past_nq_untouched(px_gpu, stream):
+    # A 256-row f16 workgroup with Nq = 128 computes rows 128..255 from zero
+    # queries but must not store them.
+    px = px_gpu
+    Nq, Nk, D = 128, 128, 64
+    q, _, _ = _inputs((Nq, D), 16, 21)
+    _, k, v = _inputs((Nk, D), 16, 31)
+    dq, dk, dv = (_upload(px, t, 16) for t in (q, k, v))
+    sentinel = np.full(2 * Nq * D, 0x7bff, np.uint16)  # f16 max, not a softmax output
+    do = px.DeviceBuffer.from_array(sentinel)
+    px.launch_flash(stream, px.FLASH_FP16, dq.ptr, dk.ptr, dv.ptr, do.ptr, Nq, Nk, D, 0.125)
+    stream.synchronize()
+    out = do.download(np.uint16, 2 * Nq * D)
+    assert np.array_equal(out[Nq * D:], sentinel[Nq * D:])
+    got = oracle.f16_to_f32(out[:Nq * D]).reshape(Nq, D)
+    assert _rel(got, oracle.flash_rows(np.arange(Nq), q, k, v, 0.125)) < TOL[16]
+
+
+@pytest.mark.parametrize("grid_x", [1, 5])
+def test_flash16_bh_any_grid(px_gpu, stream, grid_x):
+    # The bh entry walks (head, row block) work items block-stride: a grid with
+    # fewer workgroups than items (LDS ring reused across items) or more
+    # (idle workgroups) gives the grid_for result bit for bit.
+    px = px_gpu
+    BH, N, D = 3, 512, 64
+    q, k, v = _inputs((BH, N, D), 16, 41)
+    dq, dk, dv = (_upload(px, t, 16) for t in (q, k, v))
+    dref, dgot = px.DeviceBuffer(BH * N * D * 2), px.DeviceBuffer(BH * N * D * 2)
+    px.launch_flash_bh(stream, px.FLASH_FP16_BH, dq.ptr, dk.ptr, dv.ptr, dref.ptr, BH, N, N, D, 0.125)
+    fn = px.builtin_function(px.FLASH_FP16_BH)
+    px.compute(fn, 64, [(t.ptr, (BH, N, D)) for t in (dq, dk, dv, dgot)],
+               [(4, 4, px.f32_bits(0.125))], (grid_x, 1, 1), (256, 1, 1), stream)
+    stream.synchronize()
+    assert np.array_equal(dgot.download(np.uint16, BH * N * D), dref.download(np.uint16, BH * N * D))
