@@ -36,6 +36,7 @@ PEAK_FP32_TFLOPS = 157.3
 
 GEMM_FLOP = 2 * 4096 ** 3 + 4096 ** 2          # main.rs:591
 FLASH_FLOP = 4 * 4096 * 4096 * 64 * 64         # main.rs:1032, x 64 heads
+FLASH_EXPS = 4096 * 4096 * 64                  # one exp per score (secondary bound)
 SAXPY_BYTES = 12 * 4096 * 4096                 # read x, read y, write y
 # back-to-back launches per kernel per step
 REPS = {"saxpy_fp32": 8, "gemm_fp32": 2, "gemm_fp16tc_fp32acc": 2, "gemm_fp16": 2,
@@ -49,12 +50,14 @@ def log(*a):
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--kernels", default="all",
                     help="comma list of saxpy_fp32,gemm_fp32,gemm_fp16tc_fp32acc,gemm_fp16,"
                          "flash_fp32,flash_fp16")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    ap.add_argument("--no-cluster", action="store_true",
+                    help="skip the one-pod matmul_cluster job (16384^3 f32 from 3 GiB of files)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 3 device-to-device copies of 256 MiB (the plain copy the "
@@ -175,6 +178,67 @@ def cpu_baseline(seconds):
                       f"in {el:.1f} s"}
 
 
+def cpu_other_legs():
+    """The other kernels' CPU counterparts (oracle, on the host cores) and the
+    reference-style 64-sample f64 GEMM check (main.rs:386-445), each timed on
+    a bounded sample: a few seconds in all."""
+    import oracle
+    out = {"nproc": os.cpu_count(), "omp_threads": oracle.num_threads()}
+    n = 4096 * 4096
+    x, y = oracle.lcg_f32(1, n), oracle.lcg_f32(2, n)
+    t0 = time.perf_counter()
+    for _ in range(3):
+        oracle.saxpy(np.float32(2.5), x, y)
+    el = (time.perf_counter() - t0) / 3
+    out["saxpy_fp32"] = {"value": round(12 * n / el / 1e9, 2), "unit": "GB/s", "cores": 1,
+                         "kind": "port", "sample": f"orc_saxpy (scalar, volatile product so "
+                                                   f"nothing is contracted), full n = {n}, 3 runs"}
+    heads, S, D = 16, 4096, 64
+    q, k, v = (oracle.normal_f32(s, heads * S * D).reshape(heads, S, D) for s in (1, 2, 3))
+    t0 = time.perf_counter()
+    oracle.flash_f32(q, k, v, 0.125)
+    el = time.perf_counter() - t0
+    out["flash_fp32"] = {"value": round(4 * S * S * D * heads / el / 1e12, 4), "unit": "TFLOP/s",
+                         "cores": oracle.num_threads(), "kind": "port",
+                         "sample": f"orc_flash_f32 (f32, OpenMP), {heads} of the 64 heads "
+                                   f"of 4096x4096x64 in {el:.2f} s"}
+    M = 4096
+    A = oracle.lcg_f32(1, M * M).reshape(M, M)
+    B = oracle.lcg_f32(2, M * M).reshape(M, M)
+    C = oracle.lcg_f32(3, M * M).reshape(M, M)
+    r, c = oracle.sample_points(M, M, 64)
+    t0 = time.perf_counter()
+    oracle.gemm_points(r, c, A, B, C, 0.125, 1.5)
+    out["gemm_check_64_samples_s"] = round(time.perf_counter() - t0, 4)
+    return out
+
+
+def cluster_leg(px):
+    """One pod running the matmul_cluster segment: 16384^3 f32, supertiles
+    4096 / 8192 / 4096, A/B/C from Lcg-seeded files.  COMPUTE-only TFLOP/s
+    from the pod's per-launch events; end-to-end wall time separately."""
+    import shutil
+    import tempfile
+    from phobos_amd import cluster
+    M = N = K = 16384
+    work = tempfile.mkdtemp(prefix="phx_bench_cluster_")
+    try:
+        t0 = time.perf_counter()
+        stats, _, instrs = cluster.run_matmul_job(work, M, N, K, 4096, 8192, 4096, 0.125, 1.5)
+        job_s = time.perf_counter() - t0
+    finally:
+        shutil.rmtree(work, ignore_errors=True)
+    flop = 2 * M * N * K
+    return {"workload": "matmul_cluster, one pod: C = 0.125*A@B + 1.5*C, 16384^3 f32, "
+                        "supertiles 4096/8192/4096, Lcg seeds 1/2/3 in file:// tensors",
+            "compute_tflops": round(flop / (stats["compute_ns"] / 1e9) / 1e12, 2),
+            "compute_ms": round(stats["compute_ns"] / 1e6, 2),
+            "segment_wall_ms": round(stats["wall_ns"] / 1e6, 2),
+            "io_ms": round(stats["io_ns"] / 1e6, 2),
+            "job_wall_s_incl_input_files": round(job_s, 2),
+            "ops": {k: stats[k] for k in ("alloc", "load", "compute", "store", "free")}}
+
+
 def load_traffic():
     p = os.path.join(ROOT, "profiles", "traffic.json")
     if os.path.exists(p):
@@ -250,16 +314,27 @@ def main():
                          "frac": round(val / k.peak, 4),
                          "traffic": traffic.get(k.name)},
         }
+        if k.name.startswith("flash"):
+            kern[k.name]["exp_rate"] = {"exps": FLASH_EXPS,
+                                        "value": round(FLASH_EXPS / (avg / 1e3) / 1e9, 1),
+                                        "unit": "Gexp/s"}
         log(f"{k.name:22s} avg {avg:8.4f} ms  min {t.min():8.4f} ms  "
             f"{val:10.2f} {k.unit}  ({100 * val / k.peak:5.1f}% of peak)")
 
     head = "gemm_fp16tc_fp32acc"
     hk = kern.get(head) or next(iter(kern.values()))
-    cpu = None
+    cluster_res = None
+    if not args.no_cluster:
+        log("matmul_cluster one-pod job ...")
+        cluster_res = cluster_leg(px)
+        log(f"matmul_cluster: {cluster_res}")
+    cpu = cpu_more = None
     if not args.no_cpu:
         log("cpu baseline ...")
         cpu = cpu_baseline(args.cpu_seconds)
         log(f"cpu baseline: {cpu}")
+        cpu_more = cpu_other_legs()
+        log(f"cpu legs: {cpu_more}")
     out = {
         "metric": "achieved TFLOPS & % peak: gemm_fp16tc 4096^3, flash_fp16; saxpy HBM GB/s",
         "value": hk["value"],
@@ -281,7 +356,9 @@ def main():
                    "global_batch": 1, "seq_len": 4096, "parallelism": "none (1 GPU)"},
         "roofline": hk["roofline"],
         "cpu_baseline": cpu,
+        "cpu_legs": cpu_more,
         "kernels": kern,
+        "matmul_cluster": cluster_res,
         "device": info,
     }
     print(json.dumps(out), flush=True)
