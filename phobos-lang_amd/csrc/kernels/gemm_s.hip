@@ -17,84 +17,234 @@
 // two agree to f32 summation-order rounding (and exactly on integer data).
 //
 // MI355X design
-//   * 128x128 output tile, K step 32, 256 threads = 4 waves (2x2) of 64x64,
-//     each 2x2 v_mfma_f32_32x32x2_f32 tiles (64 accumulators).  LDS is 2 x 32
-//     KiB, so two workgroups share a CU.
+//   * 256x256 output tile per workgroup, one workgroup per CU, 4 waves in a
+//     2x2 arrangement, each owning 128x128 = 4x4 v_mfma_f32_32x32x2_f32 tiles
+//     whose 256 accumulators live in AGPRs.  K step 16: 128 MFMAs (8192
+//     matrix-core cycles) per wave per step, so one barrier per step costs
+//     little.  Tiles that cross M or N are computed from zero-filled loads and
+//     stored masked, so M and N only need to be multiples of 128.
 //   * The MFMA's 2-wide k slice is permuted so that a lane's four consecutive
-//     MFMAs read four consecutive k from one ds_read_b128: lane group g of MFMA
-//     s uses k = 8q + 4g + s.  A is staged As[m][k], B transposed to Bs[n][k]
-//     (a free 4x4 register transpose); 128-byte rows with the 16-byte chunk
-//     XOR-swizzled by ((row >> 1) & 7) keep writes and reads conflict free
-//     on the 64-bank LDS.
-//   * Double-buffered LDS with the next K step's loads in flight during the
-//     current step's MFMAs; XCD-aware grouped tile order as in gemm_h.hip.
+//     MFMAs read four consecutive k: lane group g of MFMA s uses k = 8q + 4g +
+//     s.  A is staged As[m][k] (64-byte rows, 16-byte chunks XOR (row>>2)&3),
+//     so an A operand for 4 MFMAs is one ds_read_b128.  B stays row-major
+//     Bs[k][n] (1 KiB rows); its operand is four ds_read_b32 (one per k), and
+//     rows whose k differs by 4 (the two lane groups) are offset by 128 bytes
+//     (chunk XOR 8 when bit 2 of k is set), so all 64 lanes hit distinct banks.
+//   * Both operands are copied global -> LDS directly (buffer_load ... lds, 16
+//     bytes per lane) into a ring of 3 stages of 32 KiB; step k+3 is issued
+//     into the stage step k just released.  Copies of steps past K read an
+//     empty buffer resource (zeros), which keeps every wait count constant.
+//   * Software pipeline as in the f16 GEMM: the MFMAs of k-group 0 run while
+//     group 1's operands are read; then the wait for the next step and the
+//     barrier; then group 1's MFMAs while the next step's group-0 operands are
+//     read and the copy of step k+3 is issued.
+//   * Workgroups are renumbered XCD-major and grouped 4 tile-rows deep.
 #include "phx_common.h"
 
-#define BM PHX_S_BM
-#define BN PHX_S_BN
-#define BK PHX_S_BK
+#define BM PHX_S_TILE
+#define BN PHX_S_TILE
+#define BK 16
 #define NT PHX_S_THREADS
-#define WM 64
-#define WN 64
+#define WM 128
+#define WN 128
 #define GROUP_M 4
-#define LDS_ROW_BYTES (BK * 4)
-#define LDS_TILE_BYTES (BM * LDS_ROW_BYTES)
 
-__device__ __forceinline__ uint32_t lds_off(uint32_t row, uint32_t chunk) {
-    return row * LDS_ROW_BYTES + ((chunk ^ ((row >> 1) & 7)) << 4);
+#define A_ROW_BYTES (BK * 4)             // 64
+#define B_ROW_BYTES (BN * 4)             // 1024
+#define A_BYTES (BM * A_ROW_BYTES)       // 16 KiB
+#define B_BYTES (BK * B_ROW_BYTES)       // 16 KiB
+#define STAGE_BYTES (A_BYTES + B_BYTES)  // 32 KiB
+#define NSTG 3
+#define DMA_PER_STEP 8                   // copies per wave per K step (4 A + 4 B)
+#define EP_RP 8                          // epilogue rows per pass
+#define EP_PITCH 136                     // epilogue LDS row pitch (floats)
+
+typedef __attribute__((address_space(3))) void *phx_lds_vp;
+
+#define PHX_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14))
+#define PHX_WAIT_VM_LGKM0(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (((n) >> 4) << 14))
+#define SGB(mask, n) __builtin_amdgcn_sched_group_barrier(mask, n, 0)
+#define G_MFMA 0x008
+#define G_VMEM 0x020
+#define G_DSR 0x100
+
+__device__ __forceinline__ uint32_t a_off(uint32_t row, uint32_t chunk) {
+    return row * A_ROW_BYTES + ((chunk ^ ((row >> 2) & 3)) << 4);
+}
+__device__ __forceinline__ uint32_t b_off(uint32_t row, uint32_t chunk) {
+    return row * B_ROW_BYTES + ((chunk ^ (((row >> 2) & 1) << 3)) << 4);
 }
 
-struct Stage {
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t phx_rsrc(const void *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes,
+                                             0x00020000);
+}
+
+// Operands of k-group q (k = 8q .. 8q+7) for this wave: a[i] = A row wm +
+// 32i + lane%32, k = 8q + 4g .. +3; b[j][s] = B[8q + 4g + s][wn + 32j + lane%32].
+struct Frags {
     phx_f4 a[4];
-    phx_f4 b[4];
+    float b[4][4];
 };
 
-__device__ __forceinline__ void load_stage(Stage &st, const float *A, int64_t lda, const float *B,
-                                           int64_t ldb, uint32_t m0, uint32_t n0, uint32_t k0,
-                                           uint32_t tid) {
-    const uint32_t ar = tid >> 3, ac = tid & 7;
+__device__ __forceinline__ void read_frags(Frags &f, const char *stage, uint32_t q, uint32_t wm,
+                                           uint32_t wn, uint32_t lane) {
+    const char *As = stage, *Bs = stage + A_BYTES;
+    const uint32_t lrow = lane & 31, g = lane >> 5;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-        st.a[i] = *(const phx_f4 *)(A + (int64_t)(m0 + i * 32 + ar) * lda + k0 + ac * 4);
-    const uint32_t bk = tid & 7, bn = tid >> 3;
+        f.a[i] = *(const phx_f4 *)(As + a_off(wm + 32 * i + lrow, 2 * q + g));
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const uint32_t row = 8 * q + 4 * g + s, col = wn + 32 * j + lrow;
+            f.b[j][s] = *(const float *)(Bs + b_off(row, col >> 2) + 4 * (col & 3));
+        }
+}
+
+// MFMA order: s outermost, then (i, j): 16 independent accumulators between
+// two updates of the same one.
+__device__ __forceinline__ void mfma_all(phx_f16v (&acc)[4][4], const Frags &f) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(f.a[i][s], f.b[j][s], acc[i][j],
+                                                                 0, 0, 0);
+}
+
+// Copies K step k0 of A and B into stage dst.  A: copy i of wave w covers
+// rows 64w + 16i + lane/4 (lane's physical chunk lane%4); B: copy i covers
+// row 4w + i (lane's physical chunk = lane).  Each lane fetches the logical
+// chunk its swizzled slot holds.  Rows past M read zeros.
+__device__ __forceinline__ void dma_step(char *dst, const float *A, int64_t lda, const float *B,
+                                         int64_t ldb, int64_t M, int64_t N, int64_t K, uint32_t m0,
+                                         uint32_t n0, uint32_t k0, uint32_t voa, uint32_t vob0,
+                                         uint32_t vob1, uint32_t wave) {
+    const bool in = (int64_t)k0 < K;
+    const int64_t mrows = M - m0 < BM ? M - m0 : BM;
+    const __amdgpu_buffer_rsrc_t ra = phx_rsrc(
+        A + (int64_t)m0 * lda + (in ? k0 : 0), in ? (uint32_t)(((mrows - 1) * lda + BK) * 4) : 0);
+    // B rows are full 1 KiB reads even when the tile crosses N: columns past
+    // N land in output columns that are not stored; the resource ends at the
+    // matrix's last element.
+    const int64_t brem = (K - (in ? k0 : 0) - 1) * ldb + (N - n0);
+    const uint32_t bbytes = (uint32_t)((brem < (BK - 1) * ldb + BN ? brem : (BK - 1) * ldb + BN) * 4);
+    const __amdgpu_buffer_rsrc_t rb =
+        phx_rsrc(B + (int64_t)(in ? k0 : 0) * ldb + n0, in ? bbytes : 0);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-        st.b[i] = *(const phx_f4 *)(B + (int64_t)(k0 + bk * 4 + i) * ldb + n0 + bn * 4);
-}
-
-__device__ __forceinline__ void store_stage(const Stage &st, char *As, char *Bs, uint32_t tid) {
-    const uint32_t ar = tid >> 3, ac = tid & 7;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            ra, (phx_lds_vp)(dst + (wave * 256 + i * 64) * 16), 16, voa,
+            (int)((uint32_t)((wave * 64 + i * 16) * lda) * 4), 0, 0);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *(phx_f4 *)(As + lds_off(i * 32 + ar, ac)) = st.a[i];
-    const uint32_t bk = tid & 7, bn = tid >> 3;
-    phx_f4 c0 = {st.b[0].x, st.b[1].x, st.b[2].x, st.b[3].x};
-    phx_f4 c1 = {st.b[0].y, st.b[1].y, st.b[2].y, st.b[3].y};
-    phx_f4 c2 = {st.b[0].z, st.b[1].z, st.b[2].z, st.b[3].z};
-    phx_f4 c3 = {st.b[0].w, st.b[1].w, st.b[2].w, st.b[3].w};
-    *(phx_f4 *)(Bs + lds_off(bn * 4 + 0, bk)) = c0;
-    *(phx_f4 *)(Bs + lds_off(bn * 4 + 1, bk)) = c1;
-    *(phx_f4 *)(Bs + lds_off(bn * 4 + 2, bk)) = c2;
-    *(phx_f4 *)(Bs + lds_off(bn * 4 + 3, bk)) = c3;
+    for (int i = 0; i < 4; ++i)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rb, (phx_lds_vp)(dst + A_BYTES + (wave * 4 + i) * B_ROW_BYTES), 16,
+            ((wave * 4 + i) >> 2) & 1 ? vob1 : vob0, (int)((uint32_t)((wave * 4 + i) * ldb) * 4),
+            0, 0);
 }
 
-// STEP: cluster step leaf (implicit beta 1), else the plain gemm epilogue.
+__device__ __forceinline__ void k_step(phx_f16v (&acc)[4][4], Frags &F0, Frags &F1, char *cur,
+                                       const char *nxt, const float *A, int64_t lda,
+                                       const float *B, int64_t ldb, int64_t M, int64_t N,
+                                       int64_t K, uint32_t m0, uint32_t n0, uint32_t kt,
+                                       uint32_t voa, uint32_t vob0, uint32_t vob1, uint32_t wm,
+                                       uint32_t wn, uint32_t wave, uint32_t lane) {
+    read_frags(F1, cur, 1, wm, wn, lane);
+    mfma_all(acc, F0);
+#pragma unroll
+    for (int i = 0; i < 64; ++i) {
+        SGB(G_MFMA, 1);
+        if (i < 20) SGB(G_DSR, 1);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    PHX_WAIT_VM_LGKM0((NSTG - 2) * DMA_PER_STEP);  // own copies of kt+1 landed, reads of cur done
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(F0, nxt, 0, wm, wn, lane);
+    dma_step(cur, A, lda, B, ldb, M, N, K, m0, n0, (kt + NSTG) * BK, voa, vob0, vob1, wave);
+    mfma_all(acc, F1);
+#pragma unroll
+    for (int i = 0; i < 64; ++i) {
+        SGB(G_MFMA, 1);
+        if (i < 20) SGB(G_DSR, 1);
+        if (i >= 20 && i < 28) SGB(G_VMEM, 1);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// Epilogue: per wave, 16 passes of 8 rows x 128 columns through a private
+// LDS region; a lane then moves 4 consecutive values of a row.  STEP: the
+// cluster step leaf (C += alpha*acc), else C = alpha*acc + beta*C (C not read
+// when beta == 0).
+template <bool STEP>
+__device__ __forceinline__ void epilogue(const phx_f16v (&acc)[4][4], float *ep_all, float *C,
+                                         int64_t ldc, int64_t M, int64_t N, uint32_t m0,
+                                         uint32_t n0, uint32_t wm, uint32_t wn, float alpha,
+                                         float beta, uint32_t wave, uint32_t lane) {
+    const uint32_t lrow = lane & 31, lgrp = lane >> 5;
+    float *ep = ep_all + wave * (EP_RP * EP_PITCH);
+#pragma unroll
+    for (int pass = 0; pass < WM / EP_RP; ++pass) {
+        const int i = (pass * EP_RP) / 32;
+        const int r0 = ((pass * EP_RP) % 32) / 2;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = r0; r < r0 + EP_RP / 2; ++r)
+                ep[(8 * (r >> 2) + 4 * lgrp + (r & 3) - 2 * r0) * EP_PITCH + 32 * j + lrow] =
+                    alpha * acc[i][j][r];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int rr = 0; rr < EP_RP / 2; ++rr) {
+            const uint32_t row = rr * 2 + (lane >> 5), c4 = (lane & 31) * 4;
+            const int64_t grow = (int64_t)m0 + wm + pass * EP_RP + row;
+            const int64_t gcol = (int64_t)n0 + wn + c4;
+            if (grow < M && gcol < N) {
+                const phx_f4 v = *(const phx_f4 *)(ep + row * EP_PITCH + c4);
+                float *dst = C + grow * ldc + gcol;
+                phx_f4 o = v;
+                if (STEP) {
+                    o = v + *(const phx_f4 *)dst;
+                } else if (beta != 0.0f) {
+                    const phx_f4 c = *(const phx_f4 *)dst;
+                    o = v + beta * c;
+                }
+                *(phx_f4 *)dst = o;
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+}
+
 template <bool STEP>
 __device__ __forceinline__ void gemm_s_body(const float *A, int64_t lda, const float *B,
                                             int64_t ldb, float *C, int64_t ldc, int64_t M,
                                             int64_t N, int64_t K, float alpha, float beta,
-                                            char (*lds)[2][LDS_TILE_BYTES]) {
+                                            char *stg0, char *stg1, char *stg2) {
+    char *const S[NSTG] = {stg0, stg1, stg2};
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63;
-    const uint32_t wave = tid >> 6;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t wm = (wave >> 1) * WM;
     const uint32_t wn = (wave & 1) * WN;
-    const uint32_t tiles_n = (uint32_t)(N / BN);
-    const uint32_t tiles_m = (uint32_t)(M / BM);
+    const uint32_t tiles_n = (uint32_t)((N + BN - 1) / BN);
+    const uint32_t tiles_m = (uint32_t)((M + BM - 1) / BM);
     const uint32_t ntiles = tiles_m * tiles_n;
     const uint32_t nblk = phx_block_count();
     const uint32_t nk = (uint32_t)(K / BK);
-    const uint32_t lrow = lane & 31;
-    const uint32_t lgrp = lane >> 5;
+    const uint32_t voa =
+        (uint32_t)(((lane >> 2) * lda + 4 * ((lane & 3) ^ ((lane >> 4) & 3))) * 4);
+    const uint32_t vob0 = lane * 16;
+    const uint32_t vob1 = (lane ^ 8) * 16;
 
     for (uint32_t t = phx_block_linear(); t < ntiles; t += nblk) {
         const uint32_t ts = nblk == ntiles ? phx_xcd_swizzle(t, ntiles) : t;
@@ -105,104 +255,67 @@ __device__ __forceinline__ void gemm_s_body(const float *A, int64_t lda, const f
         const uint32_t tn = (ts % gsz) / gm;
         const uint32_t m0 = tm * BM, n0 = tn * BN;
 
-        phx_f16v acc[2][2];
+        phx_f16v acc[4][4];
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
+            for (int j = 0; j < 4; ++j)
                 acc[i][j] = (phx_f16v){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-
-        Stage st;
-        load_stage(st, A, lda, B, ldb, m0, n0, 0, tid);
-        store_stage(st, lds[0][0], lds[0][1], tid);
+        Frags F0, F1;
+#pragma unroll
+        for (int p = 0; p < NSTG; ++p)
+            dma_step(S[p], A, lda, B, ldb, M, N, K, m0, n0, p * BK, voa, vob0, vob1, wave);
+        PHX_WAIT_VMCNT((NSTG - 1) * DMA_PER_STEP);
+        __builtin_amdgcn_s_barrier();
+        read_frags(F0, stg0, 0, wm, wn, lane);
+        uint32_t kt = 0;
+        for (; kt + NSTG <= nk; kt += NSTG) {
+#pragma unroll
+            for (int u = 0; u < NSTG; ++u)
+                k_step(acc, F0, F1, S[u], S[(u + 1) % NSTG], A, lda, B, ldb, M, N, K, m0, n0,
+                       kt + u, voa, vob0, vob1, wm, wn, wave, lane);
+        }
+#pragma unroll
+        for (int u = 0; u < NSTG - 1; ++u)
+            if (kt + u < nk)
+                k_step(acc, F0, F1, S[u], S[(u + 1) % NSTG], A, lda, B, ldb, M, N, K, m0, n0,
+                       kt + u, voa, vob0, vob1, wm, wn, wave, lane);
+        PHX_WAIT_VMCNT(0);
         __syncthreads();
-
-        for (uint32_t kt = 0; kt < nk; ++kt) {
-            const uint32_t cur = kt & 1;
-            if (kt + 1 < nk) load_stage(st, A, lda, B, ldb, m0, n0, (kt + 1) * BK, tid);
-            const char *As = lds[cur][0];
-            const char *Bs = lds[cur][1];
-#pragma unroll
-            for (uint32_t q = 0; q < BK / 8; ++q) {
-                const uint32_t chunk = 2 * q + lgrp;
-                phx_f4 af[2], bf[2];
-#pragma unroll
-                for (int i = 0; i < 2; ++i)
-                    af[i] = *(const phx_f4 *)(As + lds_off(wm + i * 32 + lrow, chunk));
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    bf[j] = *(const phx_f4 *)(Bs + lds_off(wn + j * 32 + lrow, chunk));
-#pragma unroll
-                for (int s = 0; s < 4; ++s)
-#pragma unroll
-                    for (int i = 0; i < 2; ++i)
-#pragma unroll
-                        for (int j = 0; j < 2; ++j)
-                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][s], bf[j][s],
-                                                                             acc[i][j], 0, 0, 0);
-            }
-            if (kt + 1 < nk) store_stage(st, lds[cur ^ 1][0], lds[cur ^ 1][1], tid);
-            __syncthreads();
-        }
-
-        // acc[i][j][r]: row = 8*(r/4) + 4*lgrp + r%4, col = lrow
-        if (STEP || beta != 0.0f) {
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const uint32_t col = n0 + wn + j * 32 + lrow;
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const uint32_t row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * lgrp + (r & 3);
-                        float *pc = C + (int64_t)row * ldc + col;
-                        float v = alpha * acc[i][j][r];
-                        float cb = STEP ? *pc : beta * *pc;
-                        *pc = v + cb;
-                    }
-                }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const uint32_t col = n0 + wn + j * 32 + lrow;
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const uint32_t row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * lgrp + (r & 3);
-                        C[(int64_t)row * ldc + col] = alpha * acc[i][j][r];
-                    }
-                }
-        }
+        epilogue<STEP>(acc, (float *)stg0, C, ldc, M, N, m0, n0, wm, wn, alpha, beta, wave, lane);
+        __syncthreads();
     }
 }
 
 #define GEMM_S_PRELUDE                                                                        \
-    __shared__ __attribute__((aligned(16))) char lds[2][2][LDS_TILE_BYTES];                   \
+    __shared__ __attribute__((aligned(16))) char stg0[STAGE_BYTES];                           \
+    __shared__ __attribute__((aligned(16))) char stg1[STAGE_BYTES];                           \
+    __shared__ __attribute__((aligned(16))) char stg2[STAGE_BYTES];                           \
     const int64_t M = a_s0, K = a_s1, N = b_s1;                                               \
-    if (blockDim.x != NT || M % BM || N % BN || K % BK || M <= 0 || N <= 0 || K <= 0 ||       \
-        b_s0 != K || c_s0 != M || c_s1 != N || a_st1 != 1 || b_st1 != 1 || c_st1 != 1)       \
+    if (blockDim.x != NT || M % PHX_S_BM || N % PHX_S_BN || K % PHX_S_BK || M <= 0 ||        \
+        N <= 0 || K <= 0 || b_s0 != K || c_s0 != M || c_s1 != N || a_st1 != 1 || b_st1 != 1 || \
+        c_st1 != 1)                                                                           \
         return;
 
 #ifdef PHX_GEMM_FP32
-extern "C" __global__ __launch_bounds__(NT, 2) void gemm(PHX_MEMREF2(float, a, int32_t),
+extern "C" __global__ __launch_bounds__(NT, 1) void gemm(PHX_MEMREF2(float, a, int32_t),
                                                           PHX_MEMREF2(float, b, int32_t),
                                                           PHX_MEMREF2(float, c, int32_t),
                                                           float alpha, float beta) {
     GEMM_S_PRELUDE
     gemm_s_body<false>(a_ptr + a_off, a_st0, b_ptr + b_off, b_st0, c_ptr + c_off, c_st0, M, N, K,
-                       alpha, beta, lds);
+                       alpha, beta, stg0, stg1, stg2);
 }
 #endif
 
 #ifdef PHX_MATMUL_CLUSTER
-extern "C" __global__ __launch_bounds__(NT, 2) void matmul(PHX_MEMREF2(float, a, int32_t),
+extern "C" __global__ __launch_bounds__(NT, 1) void matmul(PHX_MEMREF2(float, a, int32_t),
                                                             PHX_MEMREF2(float, b, int32_t),
                                                             PHX_MEMREF2(float, c, int32_t),
                                                             float alpha, float beta) {
     GEMM_S_PRELUDE
     gemm_s_body<true>(a_ptr + a_off, a_st0, b_ptr + b_off, b_st0, c_ptr + c_off, c_st0, M, N, K,
-                      alpha, beta, lds);
+                      alpha, beta, stg0, stg1, stg2);
 }
 
 // C = fl(beta * C) over a [M, N] tile: an HBM stream of 8 bytes per element.

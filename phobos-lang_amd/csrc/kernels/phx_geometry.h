@@ -21,10 +21,13 @@
 #define PHX_H_BK 32
 #define PHX_H_THREADS 256
 
-// f32 GEMM (gemm_fp32, cluster matmul): 128x128 output tile, K step 32,
-// 256 threads = 4 waves of 64x64.
+// f32 GEMM (gemm_fp32, cluster matmul): M and N must be multiples of
+// PHX_S_BM / PHX_S_BN and K of PHX_S_BK; a workgroup computes a
+// PHX_S_TILE x PHX_S_TILE output tile (4 waves of 128x128) and masks the part
+// past M or N.
 #define PHX_S_BM 128
 #define PHX_S_BN 128
+#define PHX_S_TILE 256
 #define PHX_S_BK 32
 #define PHX_S_THREADS 256
 

@@ -247,7 +247,8 @@ int grid_for(phx_kernel k, const int64_t *d, int nd, uint32_t grid[3], uint32_t 
         break;
     case PHX_GEMM_FP32:
     case PHX_MATMUL:
-        grid[0] = (uint32_t)((d[0] / PHX_S_BM) * (d[1] / PHX_S_BN));
+        grid[0] = (uint32_t)(((d[0] + PHX_S_TILE - 1) / PHX_S_TILE) *
+                             ((d[1] + PHX_S_TILE - 1) / PHX_S_TILE));
         break;
     case PHX_MATMUL_INIT: {
         int64_t n = d[0] * d[1];

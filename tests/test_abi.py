@@ -64,7 +64,9 @@ def test_grid_for_and_shape_checks():
     g, b = px.grid_for(px.GEMM_FP16TC_FP32ACC, [4096, 4096, 4096])
     assert g == (256, 1, 1) and b == (256, 1, 1)
     g, b = px.grid_for(px.GEMM_FP32, [4096, 4096, 4096])
-    assert g == (1024, 1, 1)
+    assert g == (256, 1, 1)
+    g, b = px.grid_for(px.GEMM_FP32, [384, 640, 32])  # 256-wide tiles, the last ones partial
+    assert g == (6, 1, 1)
     g, b = px.grid_for(px.FLASH_FP16_BH, [64, 4096, 4096, 64])
     assert g == (16, 64, 1) and b == (256, 1, 1)
     g, b = px.grid_for(px.FLASH_FP32_BH, [64, 4096, 4096, 64])
@@ -72,7 +74,7 @@ def test_grid_for_and_shape_checks():
     g, b = px.grid_for(px.FLASH_FP16, [384, 1024, 64])  # 256-row workgroups, last one half full
     assert g == (2, 1, 1)
     g, b = px.grid_for(px.MATMUL, [4096, 8192, 4096])
-    assert g == (32 * 64, 1, 1)
+    assert g == (16 * 32, 1, 1)
     assert px.check_shape(px.GEMM_FP16, [4096, 4096, 4096]) == 0
     assert px.check_shape(px.GEMM_FP16, [4096, 100, 4096]) == px.PHX_E_INVALID
     assert px.check_shape(px.FLASH_FP32, [4096, 4096, 128]) == px.PHX_E_INVALID
