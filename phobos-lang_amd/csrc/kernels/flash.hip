@@ -72,7 +72,19 @@ __device__ __forceinline__ uint32_t lds_off(uint32_t row, uint32_t chunk) {
 #endif
 }
 
-__device__ __forceinline__ float shfl_xor32(float v) { return __shfl_xor(v, 32, 64); }
+
+// v = x of lane l combined with x of lane l^32: gfx950's v_permlane32_swap
+// exchanges the two 32-lane halves in one VALU op (no LDS round trip).
+__device__ __forceinline__ float xor32_max(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x),
+                                                    __builtin_bit_cast(uint32_t, x), false, false);
+    return fmaxf(__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1]));
+}
+__device__ __forceinline__ float xor32_add(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x),
+                                                    __builtin_bit_cast(uint32_t, x), false, false);
+    return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
+}
 
 #ifdef PHX_FLASH_F16
 // ---------------------------------------------------------------- f16 path
@@ -218,24 +230,66 @@ __device__ __forceinline__ void softmax_p(phx_h8 (&pf)[4], float &ps, const phx_
     ps = (part[0] + part[1]) + (part[2] + part[3]);
 }
 
-// max over a lane's 32 scores of one half (3-input max tree), then across
-// the two lane halves.
+// max over a lane's 32 scores of one half (a running chain, which the
+// compiler turns into v_max3_f32), then across the two lane halves.
 __device__ __forceinline__ float row_max(const phx_f16v (&s)[2]) {
-    float m[11];
+    float m = s[0][0];
 #pragma unroll
-    for (int j = 0; j < 10; ++j) {
-        const int a = 3 * j, b = a + 1, c = a + 2;
-        m[j] = fmaxf(s[a >> 4][a & 15], fmaxf(s[b >> 4][b & 15], s[c >> 4][c & 15]));
-    }
-    m[10] = fmaxf(s[1][14], s[1][15]);
-    const float x = fmaxf(m[0], fmaxf(m[1], m[2])), y = fmaxf(m[3], fmaxf(m[4], m[5]));
-    const float z = fmaxf(m[6], fmaxf(m[7], m[8])), w = fmaxf(m[9], m[10]);
-    const float r = fmaxf(fmaxf(x, y), fmaxf(z, w));
-    return fmaxf(r, __shfl_xor(r, 32, 64));
+    for (int r = 1; r < 16; ++r) m = fmaxf(m, s[0][r]);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) m = fmaxf(m, s[1][r]);
+    return xor32_max(m);
 }
 
 // One key block i, in order: scores, row max and lazy rescale, P and its row
 // sums, P.V.  cur = stage of block i, fill = stage that receives block i+3.
+#define SGB(mask, n) __builtin_amdgcn_sched_group_barrier(mask, n, 0)
+#define G_MFMA 0x008
+#define G_VALU 0x002
+#define G_DSR 0x100
+// Softmax of one half.  Each lane (query) raises its own running max, with a
+// select rather than a branch, when its block max exceeds it by more than
+// RESCALE_SLACK; the exps use the new max at once.  The rescale of acc and l
+// (corr = 1 on lanes that did not raise) is applied by fix_half afterwards,
+// behind a wave-uniform branch that is rarely taken.
+__device__ __forceinline__ float half_softmax(phx_h8 (&pf)[4], float &ps, bool &up,
+                                              const phx_f16v (&s)[2], float c2, float m2) {
+    const float mx = row_max(s) * c2;
+    const bool raise = mx > m2 + RESCALE_SLACK;
+    up = raise;
+    const float m2n = raise ? mx : m2;
+    softmax_p(pf, ps, s, c2, m2n);
+    return m2n;
+}
+
+__device__ __forceinline__ void fix_half(Flash16 &fs, int h, bool up, float m2n, float ps) {
+    if (__ballot(up)) {  // wave-uniform
+        const float corr = __builtin_amdgcn_exp2f(fs.m2[h] - m2n);  // 1 where not raised
+        fs.l[h] = fs.l[h] * corr;
+        fs.acc[h][0] = fs.acc[h][0] * corr;
+        fs.acc[h][1] = fs.acc[h][1] * corr;
+        fs.m2[h] = m2n;
+    }
+    fs.l[h] += xor32_add(ps);
+}
+
+// Keeps a half's P and row sum computed inside the region that interleaves
+// them with MFMAs: IR-level code sinking would otherwise move the exps past
+// the rescale branch, out of reach of the instruction scheduler's fences.
+__device__ __forceinline__ void pin_p(phx_h8 (&pf)[4], float &ps) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        phx_u4 u = __builtin_bit_cast(phx_u4, pf[c]);
+        asm volatile("" : "+v"(u));
+        pf[c] = __builtin_bit_cast(phx_h8, u);
+    }
+    asm volatile("" : "+v"(ps));
+}
+
+// One key block i with the two query halves staggered so each half's
+// softmax (VALU) runs under the other half's MFMAs:
+//   A: S_0            B: S_1 || softmax_0
+//   C: O_0 += V.P_0 || softmax_1            D: O_1 += V.P_1
 __device__ __forceinline__ void flash16_step(Flash16 &fs, const char *cur, char *fill,
                                              const T *Kp, const T *Vp, int64_t ldk, int64_t ldv,
                                              uint32_t Nk, uint32_t i, float c2, uint32_t vk0,
@@ -247,43 +301,69 @@ __device__ __forceinline__ void flash16_step(Flash16 &fs, const char *cur, char 
     __builtin_amdgcn_sched_barrier(0);
     dma_block(fill, Kp, Vp, ldk, ldv, Nk, i + 3, vk0, vk1, vv, wave);
     phx_f16v sc[2][2];
-    {
-        phx_h8 kf[2][4];
-        read_k(kf, cur, lq, g);
+    phx_h8 kf[2][4];
+    read_k(kf, cur, lq, g);
+    // A: S_0 (two interleaved chains)
 #pragma unroll
-        for (int m = 0; m < 16; ++m) mfma_s(sc, kf, fs.qf, m);
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+            sc[0][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                kf[t][s], fs.qf[0][s],
+                s ? sc[0][t] : (phx_f16v){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0}, 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    // B: S_1 || softmax_0
+    phx_h8 pf0[4], pf1[4];
+    float ps0, ps1;
+    bool up0, up1;
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+            sc[1][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                kf[t][s], fs.qf[1][s],
+                s ? sc[1][t] : (phx_f16v){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0}, 0, 0, 0);
+    const float m2n0 = half_softmax(pf0, ps0, up0, sc[0], c2, fs.m2[0]);
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+        SGB(G_MFMA, 1);
+        SGB(G_VALU, 14);
     }
-    phx_h8 pf[2][4];
+    __builtin_amdgcn_sched_barrier(0);
+    pin_p(pf0, ps0);
+    fix_half(fs, 0, up0, m2n0, ps0);
+    __builtin_amdgcn_sched_barrier(0);
+    // C: O_0 += V_i^T . P_0^T || softmax_1
+    phx_h8 vf[4][2];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const float mx = row_max(sc[h]) * c2;
-        if (__ballot(mx > fs.m2[h] + RESCALE_SLACK)) {  // wave-uniform
-            const float m2new = fmaxf(fs.m2[h], mx);
-            const float corr = __builtin_amdgcn_exp2f(fs.m2[h] - m2new);
-            fs.l[h] = fs.l[h] * corr;
-            fs.acc[h][0] = fs.acc[h][0] * corr;
-            fs.acc[h][1] = fs.acc[h][1] * corr;
-            fs.m2[h] = m2new;
-        }
-        float ps;
-        softmax_p(pf[h], ps, sc[h], c2, fs.m2[h]);
-        fs.l[h] += ps + __shfl_xor(ps, 32, 64);
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt) vf[c][dt] = read_v(cur + KV_TILE, c, dt, lane);
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt)
+            fs.acc[0][dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[c][dt], pf0[c], fs.acc[0][dt], 0, 0, 0);
+    const float m2n1 = half_softmax(pf1, ps1, up1, sc[1], c2, fs.m2[1]);
+    SGB(G_DSR, 4);
+    SGB(G_VALU, 16);
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+        SGB(G_MFMA, 1);
+        if (m < 6) SGB(G_DSR, 2);
+        SGB(G_VALU, 12);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    pin_p(pf1, ps1);
+    fix_half(fs, 1, up1, m2n1, ps1);
+    __builtin_amdgcn_sched_barrier(0);
+    // D: O_1 += V_i^T . P_1^T
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        phx_h8 vf[2];
+    for (int c = 0; c < 4; ++c)
 #pragma unroll
-        for (int dt = 0; dt < 2; ++dt) vf[dt] = read_v(cur + KV_TILE, c, dt, lane);
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-            for (int dt = 0; dt < 2; ++dt)
-                fs.acc[h][dt] =
-                    __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[dt], pf[h][c], fs.acc[h][dt], 0, 0, 0);
-    }
+        for (int dt = 0; dt < 2; ++dt)
+            fs.acc[1][dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[c][dt], pf1[c], fs.acc[1][dt], 0, 0, 0);
 }
-
-
 __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp, T *O,
                                             int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo,
                                             uint32_t Nq, uint32_t Nk, uint32_t q0, float scale,
@@ -460,7 +540,7 @@ __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp
         for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sT[0][r]);
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sT[1][r]);
-        mx = fmaxf(mx, shfl_xor32(mx));
+        mx = xor32_max(mx);
         const float m2new = fmaxf(m2, mx * c2);
         const float corr = __builtin_amdgcn_exp2f(m2 - m2new);
         float ps = 0.0f;
@@ -472,7 +552,7 @@ __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp
                 ps += p;
                 sT[t][r] = p;
             }
-        ps += shfl_xor32(ps);
+        ps = xor32_add(ps);
         l = l * corr + ps;
         m2 = m2new;
         acc[0] = acc[0] * corr;
