@@ -217,6 +217,28 @@ int phx_pod_set_kernel(phx_pod p, uint32_t kernel_id, phx_kernel k);
  * {n_alloc, n_load, n_compute, n_store, n_free, compute_ns, wall_ns, io_ns}. */
 int phx_pod_run_segment(phx_pod p, const char *segment_text, uint64_t stats[8]);
 
+/* The scheduler's wire messages, protobuf-encoded (proto3 wire format):
+ *   phx_pod_set_manifest_pb: a phobos.v1.JobManifest
+ *     (phobos-cluster/proto/v1/phobos_v1_scheduler.proto:53-76), as the pod's
+ *     server applies it (phobos-pod/src/server.rs:189-225): each TensorEntry
+ *     is registered as with phx_pod_set_tensor (f32 file:// tensors); each
+ *     KernelEntry is bound by entry-point name to a built-in leaf ("matmul",
+ *     "matmul_init", "saxpy"); other names return PHX_E_NOT_FOUND and are
+ *     bound by id with phx_pod_set_kernel.  kernel_holders are ignored (no
+ *     peer pods).
+ *   phx_pod_run_segment_pb: a phobos.v1.Segment
+ *     (phobos-cluster/proto/v1/phobos_v1_isa.proto:107-110), decoded with the
+ *     checks of segment_from_proto (phobos-cluster/src/proto.rs:193-275) and
+ *     run like phx_pod_run_segment (server.rs:239-248 -> engine.rs).  FETCH
+ *     needs a peer pod and is rejected with PHX_E_SEGMENT. */
+int phx_pod_set_manifest_pb(phx_pod p, const void *manifest, size_t bytes);
+int phx_pod_run_segment_pb(phx_pod p, const void *segment, size_t bytes, uint64_t stats[8]);
+/* Decodes an encoded phobos.v1.Segment (the same decoder) into the text form
+ * phx_pod_run_segment takes; needs no device.  `needed` (nullable) receives
+ * the text size including the NUL; text may be NULL to query it. */
+int phx_segment_pb_to_text(const void *segment, size_t bytes, char *text, size_t cap,
+                           size_t *needed);
+
 #ifdef __cplusplus
 }
 #endif

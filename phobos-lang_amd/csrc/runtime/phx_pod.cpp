@@ -62,6 +62,7 @@ struct Instr {
     uint32_t tensor = 0;          // LOAD / STORE
     Region region;                // LOAD / STORE
     uint32_t kernel = 0;          // COMPUTE
+    uint32_t serves = 0;          // FREE: expected_serves (no peer pods here)
     std::vector<std::pair<uint64_t, Mode>> args;
     std::vector<phx_scalar_arg> scalars;
     uint32_t grid[3] = {1, 1, 1}, cta[3] = {1, 1, 1};
@@ -287,8 +288,11 @@ int parse_segment(const char *text, std::vector<Instr> *out) {
                             double d = strtod(val.c_str(), nullptr);
                             memcpy(&sa.bits, &d, 8);
                         }
+                    } else if (ty == "bool") {
+                        sa.bytes = 1;
+                        sa.bits = strtoul(val.c_str(), nullptr, 0) ? 1 : 0;
                     } else {
-                        return bad("scalar type is f32|i32|i64|f64");
+                        return bad("scalar type is f32|i32|i64|f64|bool");
                     }
                     I.scalars.push_back(sa);
                 }
@@ -303,12 +307,440 @@ int parse_segment(const char *text, std::vector<Instr> *out) {
             }
         } else if (op == "FREE") {
             I.kind = OpKind::Free;
+            if (t.size() > 4) I.serves = (uint32_t)strtoul(t[4].c_str(), nullptr, 0);
         } else {
             return bad("unknown op");
         }
         out->push_back(std::move(I));
     }
     return PHX_OK;
+}
+
+// ------------------------------------------------------ protobuf decoding
+// Hand decoder of the proto3 wire format for the scheduler's messages
+// (phobos-cluster/proto/v1/phobos_v1_isa.proto, phobos_v1_scheduler.proto),
+// with the same checks as the reference's converters (proto.rs:193-275):
+// missing sub-messages and unknown enum values are errors.  Unknown fields
+// are skipped; repeated scalars are accepted packed or unpacked.
+class Pb {
+   public:
+    Pb(const void *b, size_t n) : p_((const uint8_t *)b), end_(p_ + n) {}
+    bool done() const { return p_ >= end_; }
+    bool varint(uint64_t *v) {
+        uint64_t r = 0;
+        for (int s = 0; s < 64 && p_ < end_; s += 7) {
+            const uint8_t b = *p_++;
+            r |= (uint64_t)(b & 0x7f) << s;
+            if (!(b & 0x80)) {
+                *v = r;
+                return true;
+            }
+        }
+        return false;
+    }
+    bool tag(uint32_t *field, uint32_t *wt) {
+        uint64_t t;
+        if (!varint(&t) || (t >> 3) == 0 || (t >> 3) > 0x1fffffff) return false;
+        *field = (uint32_t)(t >> 3);
+        *wt = (uint32_t)(t & 7);
+        return true;
+    }
+    bool len(Pb *sub) {
+        uint64_t l;
+        if (!varint(&l) || l > (uint64_t)(end_ - p_)) return false;
+        *sub = Pb(p_, (size_t)l);
+        p_ += l;
+        return true;
+    }
+    bool str(std::string *out) {
+        Pb s(nullptr, 0);
+        if (!len(&s)) return false;
+        out->assign((const char *)s.p_, (size_t)(s.end_ - s.p_));
+        return true;
+    }
+    bool fixed(void *out, size_t n) {
+        if ((size_t)(end_ - p_) < n) return false;
+        memcpy(out, p_, n);
+        p_ += n;
+        return true;
+    }
+    bool skip(uint32_t wt) {
+        uint64_t v;
+        Pb s(nullptr, 0);
+        switch (wt) {
+        case 0: return varint(&v);
+        case 1: return fixed(&v, 8);
+        case 2: return len(&s);
+        case 5: return fixed(&v, 4);
+        default: return false;
+        }
+    }
+    // repeated uint64, packed (wire type 2) or one element (wire type 0)
+    bool rep_u64(uint32_t wt, std::vector<uint64_t> *out) {
+        uint64_t v;
+        if (wt == 0) {
+            if (!varint(&v)) return false;
+            out->push_back(v);
+            return true;
+        }
+        Pb s(nullptr, 0);
+        if (wt != 2 || !len(&s)) return false;
+        while (!s.done()) {
+            if (!s.varint(&v)) return false;
+            out->push_back(v);
+        }
+        return true;
+    }
+
+   private:
+    const uint8_t *p_, *end_;
+};
+
+int pb_bad(const char *what) { return set_error(PHX_E_SEGMENT, "protobuf: %s", what); }
+
+// Reads a varint field of the expected wire type.
+#define PB_VARINT(var)                                       \
+    do {                                                     \
+        uint64_t v_;                                         \
+        if (wt != 0 || !m.varint(&v_)) return pb_bad(#var); \
+        var = v_;                                            \
+    } while (0)
+
+int pb_region(Pb m, Region *r) {
+    uint32_t f, wt;
+    while (!m.done()) {
+        if (!m.tag(&f, &wt)) return pb_bad("Region tag");
+        if (f == 1) {
+            if (!m.rep_u64(wt, &r->offset)) return pb_bad("Region.offset");
+        } else if (f == 2) {
+            if (!m.rep_u64(wt, &r->shape)) return pb_bad("Region.shape");
+        } else if (!m.skip(wt)) {
+            return pb_bad("Region field");
+        }
+    }
+    if (r->offset.size() != r->shape.size() || r->shape.empty()) return pb_bad("Region rank");
+    return PHX_OK;
+}
+
+int pb_storage_ref(Pb m, Instr *I, const char *who) {
+    uint32_t f, wt;
+    bool have_region = false;
+    while (!m.done()) {
+        if (!m.tag(&f, &wt)) return pb_bad("StorageReference tag");
+        if (f == 1) {
+            uint64_t t = 0;
+            PB_VARINT(t);
+            I->tensor = (uint32_t)t;
+        } else if (f == 2) {
+            Pb s(nullptr, 0);
+            if (wt != 2 || !m.len(&s)) return pb_bad("StorageReference.region");
+            if (int rc = pb_region(s, &I->region)) return rc;
+            have_region = true;
+        } else if (!m.skip(wt)) {
+            return pb_bad("StorageReference field");
+        }
+    }
+    if (!have_region) return set_error(PHX_E_SEGMENT, "%s: StorageReference.region missing", who);
+    return PHX_OK;
+}
+
+int pb_dim3(Pb m, uint32_t out[3]) {
+    uint32_t f, wt;
+    out[0] = out[1] = out[2] = 0;  // proto3 default
+    while (!m.done()) {
+        if (!m.tag(&f, &wt)) return pb_bad("Dim3 tag");
+        if (f >= 1 && f <= 3) {
+            uint64_t v = 0;
+            PB_VARINT(v);
+            out[f - 1] = (uint32_t)v;
+        } else if (!m.skip(wt)) {
+            return pb_bad("Dim3 field");
+        }
+    }
+    return PHX_OK;
+}
+
+// ScalarValue oneof -> little-endian bits and byte width (tile.rs:74-84).
+int pb_scalar_value(Pb m, phx_scalar_arg *sa) {
+    uint32_t f, wt;
+    bool have = false;
+    while (!m.done()) {
+        if (!m.tag(&f, &wt)) return pb_bad("ScalarValue tag");
+        if (f == 1 && wt == 5) {  // f32
+            uint32_t u;
+            if (!m.fixed(&u, 4)) return pb_bad("ScalarValue.f32");
+            sa->bits = u;
+            sa->bytes = 4;
+        } else if (f == 2 && wt == 1) {  // f64
+            uint64_t u;
+            if (!m.fixed(&u, 8)) return pb_bad("ScalarValue.f64");
+            sa->bits = u;
+            sa->bytes = 8;
+        } else if (f == 3 && wt == 0) {  // i32 (negative values are 10-byte varints)
+            uint64_t u;
+            if (!m.varint(&u)) return pb_bad("ScalarValue.i32");
+            sa->bits = (uint32_t)u;
+            sa->bytes = 4;
+        } else if (f == 4 && wt == 0) {  // i64
+            uint64_t u;
+            if (!m.varint(&u)) return pb_bad("ScalarValue.i64");
+            sa->bits = u;
+            sa->bytes = 8;
+        } else if (f == 5 && wt == 0) {  // bool
+            uint64_t u;
+            if (!m.varint(&u)) return pb_bad("ScalarValue.boolean");
+            sa->bits = u ? 1 : 0;
+            sa->bytes = 1;
+        } else {
+            if (!m.skip(wt)) return pb_bad("ScalarValue field");
+            continue;
+        }
+        have = true;  // a oneof: the last value on the wire wins
+    }
+    if (!have) return set_error(PHX_E_SEGMENT, "ScalarValue.value missing");
+    return PHX_OK;
+}
+
+int pb_compute(Pb m, Instr *I) {
+    uint32_t f, wt;
+    bool have_grid = false, have_cta = false;
+    while (!m.done()) {
+        if (!m.tag(&f, &wt)) return pb_bad("Compute tag");
+        Pb s(nullptr, 0);
+        if (f == 1) {
+            uint64_t k = 0;
+            PB_VARINT(k);
+            I->kernel = (uint32_t)k;
+        } else if (f == 2) {  // ComputeArgument {tile, mode}
+            if (wt != 2 || !m.len(&s)) return pb_bad("Compute.arguments");
+            uint64_t tile = 0, mode = 0;
+            uint32_t g, gwt;
+            while (!s.done()) {
+                if (!s.tag(&g, &gwt)) return pb_bad("ComputeArgument tag");
+                uint64_t v;
+                if ((g == 1 || g == 2) && gwt == 0) {
+                    if (!s.varint(&v)) return pb_bad("ComputeArgument");
+                    (g == 1 ? tile : mode) = v;
+                } else if (!s.skip(gwt)) {
+                    return pb_bad("ComputeArgument field");
+                }
+            }
+            if (mode < 1 || mode > 3)
+                return set_error(PHX_E_SEGMENT, "unknown AccessMode %llu", (unsigned long long)mode);
+            I->args.push_back({tile, mode == 1 ? Mode::Read : mode == 2 ? Mode::Write : Mode::RMW});
+        } else if (f == 3 || f == 4) {
+            if (wt != 2 || !m.len(&s)) return pb_bad("Compute.grid/cta");
+            if (int rc = pb_dim3(s, f == 3 ? I->grid : I->cta)) return rc;
+            (f == 3 ? have_grid : have_cta) = true;
+        } else if (f == 5) {  // ScalarArgument {position, value}
+            if (wt != 2 || !m.len(&s)) return pb_bad("Compute.scalars");
+            phx_scalar_arg sa{0, 0, 0};
+            bool have_value = false;
+            uint32_t g, gwt;
+            while (!s.done()) {
+                if (!s.tag(&g, &gwt)) return pb_bad("ScalarArgument tag");
+                Pb v(nullptr, 0);
+                if (g == 1 && gwt == 0) {
+                    uint64_t pos;
+                    if (!s.varint(&pos)) return pb_bad("ScalarArgument.position");
+                    sa.pos = (uint32_t)pos;
+                } else if (g == 2 && gwt == 2) {
+                    if (!s.len(&v)) return pb_bad("ScalarArgument.value");
+                    if (int rc = pb_scalar_value(v, &sa)) return rc;
+                    have_value = true;
+                } else if (!s.skip(gwt)) {
+                    return pb_bad("ScalarArgument field");
+                }
+            }
+            if (!have_value) return set_error(PHX_E_SEGMENT, "ScalarArgument.value missing");
+            I->scalars.push_back(sa);
+        } else if (!m.skip(wt)) {
+            return pb_bad("Compute field");
+        }
+    }
+    if (!have_grid) return set_error(PHX_E_SEGMENT, "Compute.grid missing");
+    if (!have_cta) return set_error(PHX_E_SEGMENT, "Compute.cta missing");
+    return PHX_OK;
+}
+
+// Operation oneof -> Instr fields.
+int pb_operation(Pb m, Instr *I) {
+    uint32_t f, wt;
+    bool have = false;
+    while (!m.done()) {
+        if (!m.tag(&f, &wt)) return pb_bad("Operation tag");
+        if (f < 1 || f > 6) {
+            if (!m.skip(wt)) return pb_bad("Operation field");
+            continue;
+        }
+        Pb s(nullptr, 0);
+        if (wt != 2 || !m.len(&s)) return pb_bad("Operation kind");
+        *I = Instr{I->iid, I->deps};  // a later kind on the wire replaces an earlier one
+        uint32_t g, gwt;
+        if (f == 3)
+            return set_error(PHX_E_SEGMENT,
+                             "FETCH (a tile from another pod) needs a peer; this executor runs "
+                             "one pod");
+        if (f == 4) {
+            I->kind = OpKind::Compute;
+            if (int rc = pb_compute(s, I)) return rc;
+            have = true;
+            continue;
+        }
+        I->kind = f == 1 ? OpKind::Alloc : f == 2 ? OpKind::Load : f == 5 ? OpKind::Store : OpKind::Free;
+        bool have_ref = false;
+        uint64_t dtype = 0;
+        while (!s.done()) {
+            if (!s.tag(&g, &gwt)) return pb_bad("op tag");
+            if (g == 1 && gwt == 0) {
+                if (!s.varint(&I->tile)) return pb_bad("op.tile");
+            } else if (f == 6 && g == 2 && gwt == 0) {
+                uint64_t v;
+                if (!s.varint(&v)) return pb_bad("Free.expected_serves");
+                I->serves = (uint32_t)v;
+            } else if (f == 1 && g == 2) {
+                if (!s.rep_u64(gwt, &I->shape)) return pb_bad("Allocate.shape");
+            } else if (f == 1 && g == 3 && gwt == 0) {
+                if (!s.varint(&dtype)) return pb_bad("Allocate.data_type");
+            } else if ((f == 2 || f == 5) && g == 2 && gwt == 2) {
+                Pb r(nullptr, 0);
+                if (!s.len(&r)) return pb_bad("StorageReference");
+                if (int rc = pb_storage_ref(r, I, f == 2 ? "Load" : "Store")) return rc;
+                have_ref = true;
+            } else if (!s.skip(gwt)) {
+                return pb_bad("op field");
+            }
+        }
+        if (f == 1) {
+            if (dtype < 1 || dtype > 7)
+                return set_error(PHX_E_SEGMENT, "unknown DataType %llu", (unsigned long long)dtype);
+            if (dtype != 2) return set_error(PHX_E_SEGMENT, "only f32 tiles (tile_store.rs:111-131)");
+            if (I->shape.empty()) return set_error(PHX_E_SEGMENT, "Allocate.shape empty");
+        }
+        if ((f == 2 || f == 5) && !have_ref)
+            return set_error(PHX_E_SEGMENT, f == 2 ? "Load.source missing" : "Store.destination missing");
+        have = true;
+    }
+    if (!have) return set_error(PHX_E_SEGMENT, "Operation.kind missing");
+    return PHX_OK;
+}
+
+int pb_segment(const void *bytes, size_t n, std::vector<Instr> *out) {
+    if (!bytes && n) return set_error(PHX_E_INVALID, "null segment bytes");
+    Pb m(bytes, n);
+    uint32_t f, wt;
+    while (!m.done()) {
+        if (!m.tag(&f, &wt)) return pb_bad("Segment tag");
+        if (f != 2) {
+            if (!m.skip(wt)) return pb_bad("Segment field");
+            continue;
+        }
+        Pb ins(nullptr, 0);
+        if (wt != 2 || !m.len(&ins)) return pb_bad("Segment.instructions");
+        Instr I;
+        bool have_op = false;
+        uint32_t g, gwt;
+        while (!ins.done()) {
+            if (!ins.tag(&g, &gwt)) return pb_bad("Instruction tag");
+            if (g == 1 && gwt == 0) {
+                if (!ins.varint(&I.iid)) return pb_bad("Instruction.iid");
+            } else if (g == 2) {
+                if (!ins.rep_u64(gwt, &I.deps)) return pb_bad("Instruction.dependencies");
+            } else if (g == 3 && gwt == 2) {
+                Pb op(nullptr, 0);
+                if (!ins.len(&op)) return pb_bad("Instruction.operation");
+                Instr J{I.iid, I.deps};
+                if (int rc = pb_operation(op, &J)) return rc;
+                const uint64_t iid = I.iid;
+                const std::vector<uint64_t> deps = I.deps;
+                I = std::move(J);
+                I.iid = iid;
+                I.deps = deps;
+                have_op = true;
+            } else if (!ins.skip(gwt)) {
+                return pb_bad("Instruction field");
+            }
+        }
+        if (!have_op)
+            return set_error(PHX_E_SEGMENT, "iid %llu: Instruction.operation missing",
+                             (unsigned long long)I.iid);
+        out->push_back(std::move(I));
+    }
+    return PHX_OK;
+}
+
+// The text form of an instruction list (the inverse of parse_segment).
+std::string render_text(const std::vector<Instr> &ins) {
+    std::string out;
+    char buf[128];
+    auto list = [](const std::vector<uint64_t> &v, char sep) {
+        std::string r;
+        for (size_t i = 0; i < v.size(); ++i) {
+            if (i) r += sep;
+            r += std::to_string((unsigned long long)v[i]);
+        }
+        return r.empty() ? std::string("-") : r;
+    };
+    for (const Instr &I : ins) {
+        out += std::to_string((unsigned long long)I.iid) + " " + list(I.deps, ',') + " ";
+        snprintf(buf, sizeof buf, "0x%llx", (unsigned long long)I.tile);
+        switch (I.kind) {
+        case OpKind::Alloc:
+            out += std::string("ALLOC ") + buf + " " + list(I.shape, 'x') + " f32";
+            break;
+        case OpKind::Load:
+        case OpKind::Store:
+            out += std::string(I.kind == OpKind::Load ? "LOAD " : "STORE ") + buf + " " +
+                   std::to_string(I.tensor) + " " + list(I.region.offset, ',') + " " +
+                   list(I.region.shape, ',');
+            break;
+        case OpKind::Compute: {
+            out += "COMPUTE " + std::to_string(I.kernel) + " ";
+            for (size_t a = 0; a < I.args.size(); ++a) {
+                snprintf(buf, sizeof buf, "%s0x%llx:%s", a ? "," : "",
+                         (unsigned long long)I.args[a].first,
+                         I.args[a].second == Mode::Read ? "r"
+                         : I.args[a].second == Mode::Write ? "w" : "rmw");
+                out += buf;
+            }
+            out += " ";
+            if (I.scalars.empty()) out += "-";
+            for (size_t k = 0; k < I.scalars.size(); ++k) {
+                const phx_scalar_arg &sa = I.scalars[k];
+                // only the width and bit pattern reach the kernel, so 4-byte
+                // values print as f32 bits and 8-byte ones as i64: both exact
+                if (sa.bytes == 1)
+                    snprintf(buf, sizeof buf, "%u:bool:%u", sa.pos, (unsigned)sa.bits);
+                else if (sa.bytes == 4)
+                    snprintf(buf, sizeof buf, "%u:f32:0x%llx", sa.pos, (unsigned long long)sa.bits);
+                else
+                    snprintf(buf, sizeof buf, "%u:i64:%lld", sa.pos, (long long)sa.bits);
+                out += (k ? "," : "") + std::string(buf);
+            }
+            snprintf(buf, sizeof buf, " %u,%u,%u %u,%u,%u", I.grid[0], I.grid[1], I.grid[2],
+                     I.cta[0], I.cta[1], I.cta[2]);
+            out += buf;
+            break;
+        }
+        case OpKind::Free:
+            out += std::string("FREE ") + buf + " " + std::to_string(I.serves);
+            break;
+        }
+        out += "\n";
+    }
+    return out;
+}
+
+// Built-in kernels a JobManifest may name (KernelEntry.name, the entry
+// point): the one-pod job's leaves (clustergen.rs:1285, 1353) and saxpy.
+// The GEMM and flash entry names are shared by several .ph kernels, so those
+// are bound by id with phx_pod_set_kernel instead.
+bool builtin_by_name(const std::string &name, phx_kernel *k) {
+    if (name == "matmul") *k = PHX_MATMUL;
+    else if (name == "matmul_init") *k = PHX_MATMUL_INIT;
+    else if (name == "saxpy") *k = PHX_SAXPY_FP32;
+    else return false;
+    return true;
 }
 
 }  // namespace
@@ -370,10 +802,85 @@ int phx_pod_set_kernel(phx_pod p, uint32_t kernel_id, phx_kernel k) {
     return PHX_OK;
 }
 
+static int run_instrs(phx_pod p, std::vector<Instr> &ins, uint64_t stats[8]);
+
 int phx_pod_run_segment(phx_pod p, const char *text, uint64_t stats[8]) {
     if (!p) return set_error(PHX_E_INVALID, "null pod");
     std::vector<Instr> ins;
     if (int rc = parse_segment(text, &ins)) return rc;
+    return run_instrs(p, ins, stats);
+}
+
+int phx_pod_run_segment_pb(phx_pod p, const void *segment, size_t bytes, uint64_t stats[8]) {
+    if (!p) return set_error(PHX_E_INVALID, "null pod");
+    std::vector<Instr> ins;
+    if (int rc = pb_segment(segment, bytes, &ins)) return rc;
+    return run_instrs(p, ins, stats);
+}
+
+int phx_pod_set_manifest_pb(phx_pod p, const void *manifest, size_t bytes) {
+    if (!p || (!manifest && bytes)) return set_error(PHX_E_INVALID, "set_manifest: bad argument");
+    Pb m(manifest, bytes);
+    uint32_t f, wt;
+    while (!m.done()) {
+        if (!m.tag(&f, &wt)) return pb_bad("JobManifest tag");
+        Pb e(nullptr, 0);
+        if ((f != 1 && f != 2) || wt != 2) {
+            if (!m.skip(wt)) return pb_bad("JobManifest field");
+            continue;  // kernel_holders and unknown fields: not used by one pod
+        }
+        if (!m.len(&e)) return pb_bad("JobManifest entry");
+        uint64_t index = 0, dtype = 2;
+        std::string uri, hash, name;
+        std::vector<uint64_t> shape;
+        uint32_t g, gwt;
+        while (!e.done()) {
+            if (!e.tag(&g, &gwt)) return pb_bad("entry tag");
+            bool ok = true;
+            if (g == 1 && gwt == 0) ok = e.varint(&index);
+            else if (f == 1 && g == 2 && gwt == 2) ok = e.str(&uri);
+            else if (f == 1 && g == 3 && gwt == 0) ok = e.varint(&dtype);
+            else if (f == 1 && g == 4) ok = e.rep_u64(gwt, &shape);
+            else if (f == 2 && g == 2 && gwt == 2) ok = e.str(&hash);
+            else if (f == 2 && g == 3 && gwt == 2) ok = e.str(&name);
+            else ok = e.skip(gwt);
+            if (!ok) return pb_bad(f == 1 ? "TensorEntry field" : "KernelEntry field");
+        }
+        if (f == 1) {
+            if (dtype != 2 && dtype != 0)
+                return set_error(PHX_E_SEGMENT, "tensor %llu: only f32 tensors (storage.rs:48-79)",
+                                 (unsigned long long)index);
+            if (int rc = phx_pod_set_tensor(p, (uint32_t)index, uri.c_str(), shape.data(),
+                                            (uint32_t)shape.size()))
+                return rc;
+        } else {
+            phx_kernel k;
+            if (!builtin_by_name(name, &k))
+                return set_error(PHX_E_NOT_FOUND,
+                                 "kernel %llu '%s' is not a built-in pod leaf; bind it with "
+                                 "phx_pod_set_kernel",
+                                 (unsigned long long)index, name.c_str());
+            if (int rc = phx_pod_set_kernel(p, (uint32_t)index, k)) return rc;
+        }
+    }
+    return PHX_OK;
+}
+
+int phx_segment_pb_to_text(const void *segment, size_t bytes, char *text, size_t cap,
+                           size_t *needed) {
+    std::vector<Instr> ins;
+    if (int rc = pb_segment(segment, bytes, &ins)) return rc;
+    const std::string t = render_text(ins);
+    if (needed) *needed = t.size() + 1;
+    if (!text || cap < t.size() + 1)
+        return text ? set_error(PHX_E_INVALID, "text buffer of %zu bytes, %zu needed", cap,
+                                t.size() + 1)
+                    : PHX_OK;
+    memcpy(text, t.c_str(), t.size() + 1);
+    return PHX_OK;
+}
+
+static int run_instrs(phx_pod p, std::vector<Instr> &ins, uint64_t stats[8]) {
     const size_t n = ins.size();
     std::unordered_map<uint64_t, size_t> by_iid;
     for (size_t i = 0; i < n; ++i) {

@@ -160,6 +160,11 @@ def lib():
                                      ctypes.POINTER(_u64), ctypes.c_uint32]
     L.phx_pod_set_kernel.argtypes = [_vp, ctypes.c_uint32, ctypes.c_int]
     L.phx_pod_run_segment.argtypes = [_vp, ctypes.c_char_p, ctypes.POINTER(_u64)]
+    L.phx_pod_set_manifest_pb.argtypes = [_vp, ctypes.c_char_p, ctypes.c_size_t]
+    L.phx_pod_run_segment_pb.argtypes = [_vp, ctypes.c_char_p, ctypes.c_size_t,
+                                         ctypes.POINTER(_u64)]
+    L.phx_segment_pb_to_text.argtypes = [ctypes.c_char_p, ctypes.c_size_t, ctypes.c_char_p,
+                                         ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]
     _LIB = L
     return L
 
@@ -411,3 +416,13 @@ def from_f16_bits(bits):
     check(lib().phx_f16_to_f32(bits.size, bits.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)),
                                out.ctypes.data_as(ctypes.POINTER(ctypes.c_float))))
     return out
+
+
+def segment_pb_to_text(data):
+    """Decodes an encoded phobos.v1.Segment into the pod's text form
+    (phx_segment_pb_to_text; no device needed)."""
+    need = ctypes.c_size_t()
+    check(lib().phx_segment_pb_to_text(data, len(data), None, 0, ctypes.byref(need)))
+    buf = ctypes.create_string_buffer(need.value)
+    check(lib().phx_segment_pb_to_text(data, len(data), buf, need.value, ctypes.byref(need)))
+    return buf.value.decode()

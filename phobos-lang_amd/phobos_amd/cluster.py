@@ -156,6 +156,89 @@ def segment_text(instrs):
     return "\n".join(lines) + "\n"
 
 
+# ------------------------------------------------------------ wire format
+# proto3 encoding of phobos.v1.Segment and JobManifest
+# (phobos-cluster/proto/v1/phobos_v1_isa.proto, phobos_v1_scheduler.proto):
+# fields in field-number order, repeated scalars packed, default values
+# omitted -- the canonical form protobuf libraries write.
+def _varint(v):
+    v &= (1 << 64) - 1
+    out = bytearray()
+    while True:
+        b = v & 0x7F
+        v >>= 7
+        out.append(b | (0x80 if v else 0))
+        if not v:
+            return bytes(out)
+
+
+def _key(field, wt):
+    return _varint((field << 3) | wt)
+
+
+def _u(field, v):
+    return _key(field, 0) + _varint(v) if v else b""
+
+
+def _msg(field, body, keep_empty=False):
+    if not body and not keep_empty:
+        return b""
+    return _key(field, 2) + _varint(len(body)) + body
+
+
+def _packed(field, vals):
+    return _msg(field, b"".join(_varint(v) for v in vals))
+
+
+_AM = {"r": 1, "w": 2, "rmw": 3}
+_OPS = {"ALLOC": 1, "LOAD": 2, "COMPUTE": 4, "STORE": 5, "FREE": 6}
+
+
+def _region(offset, shape):
+    return _packed(1, offset) + _packed(2, shape)
+
+
+def _operation(i):
+    op = i["op"]
+    if op == "ALLOC":
+        body = _u(1, i["tile"]) + _packed(2, i["shape"]) + _u(3, 2)        # DATA_TYPE_F32
+    elif op in ("LOAD", "STORE"):
+        ref = _u(1, i["tensor"]) + _msg(2, _region(i["offset"], i["shape"]), True)
+        body = _u(1, i["tile"]) + _msg(2, ref, True)
+    elif op == "COMPUTE":
+        body = _u(1, i["kernel"])
+        for t, m in i["args"]:
+            body += _msg(2, _u(1, t) + _u(2, _AM[m]), True)
+        dim = lambda d: _u(1, d[0]) + _u(2, d[1]) + _u(3, d[2])
+        body += _msg(3, dim(i["grid"]), True) + _msg(4, dim(i["cta"]), True)
+        for pos, val in i["scalars"]:
+            sv = _key(1, 5) + int(f32_bits(val)).to_bytes(4, "little")   # ScalarValue.f32
+            body += _msg(5, _u(1, pos) + _msg(2, sv, True), True)
+    else:  # FREE
+        body = _u(1, i["tile"]) + _u(2, i.get("serves", 0))
+    return _msg(_OPS[op], body, True)
+
+
+def segment_pb(instrs, segment_id=0):
+    """Encodes an instruction list as a phobos.v1.Segment."""
+    out = _u(1, segment_id)
+    for i in instrs:
+        out += _msg(2, _u(1, i["iid"]) + _packed(2, i["deps"]) + _msg(3, _operation(i), True),
+                    True)
+    return out
+
+
+def manifest_pb(tensors, kernels):
+    """Encodes a phobos.v1.JobManifest: tensors [(index, uri, shape)] (f32),
+    kernels [(index, hash, name)]."""
+    out = b""
+    for idx, uri, shape in tensors:
+        out += _msg(1, _u(1, idx) + _msg(2, uri.encode()) + _u(3, 2) + _packed(4, shape), True)
+    for idx, h, name in kernels:
+        out += _msg(2, _u(1, idx) + _msg(2, h.encode()) + _msg(3, name.encode()), True)
+    return out
+
+
 def count_ops(instrs):
     out = {}
     for i in instrs:
@@ -212,6 +295,16 @@ class Pod:
     def run(self, text):
         st = (ctypes.c_uint64 * 8)()
         check(lib().phx_pod_run_segment(self.h, text.encode(), st))
+        return dict(zip(STATS, list(st)))
+
+    def set_manifest_pb(self, data):
+        """Applies an encoded phobos.v1.JobManifest (tensors, kernels)."""
+        check(lib().phx_pod_set_manifest_pb(self.h, data, len(data)))
+
+    def run_pb(self, data):
+        """Runs an encoded phobos.v1.Segment."""
+        st = (ctypes.c_uint64 * 8)()
+        check(lib().phx_pod_run_segment_pb(self.h, data, len(data), st))
         return dict(zip(STATS, list(st)))
 
     def close(self):

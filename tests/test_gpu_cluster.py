@@ -86,3 +86,40 @@ def test_baseline_job_16384(px_gpu, tmp_path):
         assert abs(got[i, j] - want) / abs(want) < 1e-4, (i, j, got[i, j], want)
     tflops = 2 * M * N * K / (stats["compute_ns"] * 1e-9) / 1e12
     print(f"[cluster] compute {tflops:.1f} TFLOP/s, wall {stats['wall_ns'] / 1e9:.2f} s", flush=True)
+
+
+def test_wire_format_job_matches_text_job(px_gpu, tmp_path):
+    # The same one-pod job fed as the scheduler's messages: a JobManifest
+    # (tensors by index, leaves bound by entry name, server.rs:189-225) and an
+    # encoded Segment (server.rs:239-248).  The result file must equal the
+    # text-path run bit for bit.
+    M, N, K, TM, TN, TK = 512, 1024, 512, 256, 512, 256
+    text_dir, pb_dir = tmp_path / "text", tmp_path / "pb"
+    text_dir.mkdir()
+    pb_dir.mkdir()
+    _, paths_t, ins = cl.run_matmul_job(str(text_dir), M, N, K, TM, TN, TK, 0.125, 1.5)
+    shapes = {cl.A: (M, K), cl.B: (K, N), cl.C: (M, N)}
+    paths = {t: os.path.join(str(pb_dir), f"{n}.tensor") for t, n in ((cl.A, "a"), (cl.B, "b"), (cl.C, "c"))}
+    for t, seed in ((cl.A, 1), (cl.B, 2), (cl.C, 3)):
+        cl.init_tensor(paths[t], shapes[t], "random", seed)
+    manifest = cl.manifest_pb([(t, "file://" + paths[t], shapes[t]) for t in (cl.A, cl.B, cl.C)],
+                              [(cl.STEP_LEAF, "0" * 64, "matmul"), (cl.INIT_LEAF, "1" * 64, "matmul_init")])
+    pod = cl.Pod(4 * (M * K + K * N + M * N) + (1 << 20), 4)
+    try:
+        pod.set_manifest_pb(manifest)
+        stats = pod.run_pb(cl.segment_pb(ins, 1))
+    finally:
+        pod.close()
+    assert stats["compute"] == cl.count_ops(ins)["COMPUTE"]
+    got = np.fromfile(paths[cl.C], np.float32)
+    assert np.array_equal(got.view(np.uint32), np.fromfile(paths_t[cl.C], np.float32).view(np.uint32))
+
+
+def test_manifest_unknown_kernel_name_is_reported(px_gpu):
+    pod = cl.Pod(1 << 20, 1)
+    try:
+        with pytest.raises(px_gpu.PhxError) as e:
+            pod.set_manifest_pb(cl.manifest_pb([], [(0, "0" * 64, "gemm")]))
+        assert e.value.code == 1003 and "phx_pod_set_kernel" in str(e.value)
+    finally:
+        pod.close()
