@@ -192,6 +192,10 @@ int phx_arena_stats(phx_arena a, size_t *cap, size_t *bump, uint64_t *base);
 /* ------------------------------------------------------------ inputs */
 /* Lcg::unit_f32s (phobos-base/src/rng.rs:9-25) into host memory. */
 int phx_lcg_fill_f32(uint64_t seed, size_t n, float *out);
+/* The same stream continued: *state is the Lcg state (the seed before the
+ * first call) and is advanced by n draws, so a tensor can be filled chunk by
+ * chunk (phobos-tensor.rs:55-70). */
+int phx_lcg_fill_f32_stream(uint64_t *state, size_t n, float *out);
 /* Seeded N(0,1)*scale by Box-Muller over Lcg draws (this backend's input
  * convention for the BASELINE configs; the reference has no normal draw). */
 int phx_normal_fill_f32(uint64_t seed, size_t n, double scale, float *out);

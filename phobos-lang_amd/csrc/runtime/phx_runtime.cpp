@@ -598,13 +598,20 @@ int phx_flash_attention_bh(phx_stream s, phx_kernel k, uint64_t q, uint64_t kk, 
 }
 
 // ------------------------------------------------------------------ inputs
-int phx_lcg_fill_f32(uint64_t seed, size_t n, float *out) {
-    uint64_t st = seed;
+int phx_lcg_fill_f32_stream(uint64_t *state, size_t n, float *out) {
+    if (!state || (n && !out)) return set_error(PHX_E_INVALID, "lcg stream: null argument");
+    uint64_t st = *state;
     for (size_t i = 0; i < n; ++i) {
         st = st * 6364136223846793005ULL + 1442695040888963407ULL;
         out[i] = (float)(st >> 33) / 2147483648.0f - 1.0f;
     }
+    *state = st;
     return PHX_OK;
+}
+
+int phx_lcg_fill_f32(uint64_t seed, size_t n, float *out) {
+    uint64_t st = seed;
+    return phx_lcg_fill_f32_stream(&st, n, out);
 }
 
 int phx_normal_fill_f32(uint64_t seed, size_t n, double scale, float *out) {

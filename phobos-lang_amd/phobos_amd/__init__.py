@@ -160,6 +160,7 @@ def lib():
                                      ctypes.POINTER(_u64), ctypes.c_uint32]
     L.phx_pod_set_kernel.argtypes = [_vp, ctypes.c_uint32, ctypes.c_int]
     L.phx_pod_run_segment.argtypes = [_vp, ctypes.c_char_p, ctypes.POINTER(_u64)]
+    L.phx_lcg_fill_f32_stream.argtypes = [ctypes.POINTER(_u64), ctypes.c_size_t, _vp]
     L.phx_pod_set_manifest_pb.argtypes = [_vp, ctypes.c_char_p, ctypes.c_size_t]
     L.phx_pod_run_segment_pb.argtypes = [_vp, ctypes.c_char_p, ctypes.c_size_t,
                                          ctypes.POINTER(_u64)]

@@ -250,20 +250,9 @@ def count_ops(instrs):
 def init_tensor(path, shape, fill="random", seed=1, value=0.0):
     """phobos-tensor `init` (phobos-cluster/src/bin/phobos-tensor.rs:41-83):
     raw little-endian f32, filled with zeros, Lcg(seed) uniforms, a constant or
-    iota."""
-    from . import lcg_f32
-    n = int(np.prod(shape))
-    if fill == "random":
-        data = lcg_f32(seed, n)
-    elif fill == "zero":
-        data = np.zeros(n, np.float32)
-    elif fill == "const":
-        data = np.full(n, value, np.float32)
-    elif fill == "iota":
-        data = np.arange(n, dtype=np.float32)
-    else:
-        raise ValueError(fill)
-    data.tofile(path)
+    iota, written chunk by chunk."""
+    from .tensor import init
+    init("file://" + os.path.abspath(path), list(shape), fill, value, seed)
 
 
 def read_region(path, tensor_shape, offset, shape):

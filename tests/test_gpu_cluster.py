@@ -123,3 +123,30 @@ def test_manifest_unknown_kernel_name_is_reported(px_gpu):
         assert e.value.code == 1003 and "phx_pod_set_kernel" in str(e.value)
     finally:
         pod.close()
+
+
+def test_job_file_runs_on_one_pod(px_gpu, tmp_path):
+    # A matmul_cluster job file (phobos-sched job format) seeded with the
+    # phobos-tensor tool, run through phobos_amd.job, checked against the
+    # oracle at the xorshift sample points.
+    from phobos_amd import job as jb
+    from phobos_amd import tensor as tn
+    M, N, K = 512, 1024, 256
+    for name, shape, seed in (("a", f"{M}x{K}", 1), ("b", f"{K}x{N}", 2), ("c", f"{M}x{N}", 3)):
+        assert tn.main(["init", "--uri", f"file://{tmp_path}/{name}.tensor", "--shape", shape,
+                        "--fill", "random", "--seed", str(seed)]) == 0
+    p = tmp_path / "job.txt"
+    p.write_text(f"source = x\ndim M = {M}\ndim N = {N}\ndim K = {K}\n"
+                 f"tensor A = read f32 {M}x{K} file://{tmp_path}/a.tensor\n"
+                 f"tensor B = read f32 {K}x{N} file://{tmp_path}/b.tensor\n"
+                 f"tensor C = rmw f32 {M}x{N} file://{tmp_path}/c.tensor\n"
+                 "scalar alpha = f32 0.125\nscalar beta = f32 1.5\n")
+    stats = jb.run_job(jb.parse_job(str(p), read_source=False), tiles=(256, 512, 128))
+    assert stats["compute"] == 2 * 2 * (1 + 2)
+    A = oracle.lcg_f32(1, M * K).reshape(M, K)
+    B = oracle.lcg_f32(2, K * N).reshape(K, N)
+    C = oracle.lcg_f32(3, M * N).reshape(M, N)
+    got = np.fromfile(f"{tmp_path}/c.tensor", np.float32).reshape(M, N)
+    r, c = oracle.sample_points(M, N, 64)
+    want = oracle.gemm_points(r, c, A, B, C, 0.125, 1.5)
+    assert (np.abs(got[r, c] - want) / np.abs(want)).max() < 1e-4
