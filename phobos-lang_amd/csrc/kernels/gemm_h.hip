@@ -331,8 +331,17 @@ __device__ __forceinline__ void tc_step(phx_f16v (&acc)[4][4], Frags &F0, Frags 
 // reads.  Copies of K steps past the end read through an empty buffer
 // resource (zeros) into stages nobody reads, which keeps every wait count
 // constant.
+#ifdef PHX_CLOCK_PROBE
+#define PHX_PROBE_PARAMS , uint64_t &probe_wait, uint64_t &probe_bar
+#define PHX_PROBE_ARGS , probe_wait, probe_bar
+#else
+#define PHX_PROBE_PARAMS
+#define PHX_PROBE_ARGS
+#endif
 #define DMA_PER_STEP 8  // copies per wave per K step (4 A + 4 B)
+#ifndef NSTG
 #define NSTG 3
+#endif
 
 __device__ __forceinline__ void dma_step(char *dst, const TIn *A, int64_t lda, const TIn *B,
                                          int64_t ldb, int64_t K, uint32_t m0, uint32_t n0,
@@ -360,7 +369,7 @@ __device__ __forceinline__ void dma_k_step(phx_f16v (&acc)[4][4], Frags &F0, Fra
                                            const TIn *B, int64_t ldb, int64_t K, uint32_t m0,
                                            uint32_t n0, uint32_t kt, uint32_t voa, uint32_t vob0,
                                            uint32_t vob1, uint32_t wm, uint32_t wn, uint32_t wave,
-                                           uint32_t lane) {
+                                           uint32_t lane PHX_PROBE_PARAMS) {
     read_frags(F1, cur, 1, wm, wn, lane);
     mfma_all(acc, F0);
 #pragma unroll
@@ -369,8 +378,21 @@ __device__ __forceinline__ void dma_k_step(phx_f16v (&acc)[4][4], Frags &F0, Fra
         if (i < 12) SGB(G_DSR, 1);
     }
     __builtin_amdgcn_sched_barrier(0);
+#ifdef PHX_CLOCK_PROBE
+    const uint64_t pw0 = __builtin_amdgcn_s_memtime();
+#endif
     PHX_WAIT_VM_LGKM0((NSTG - 2) * DMA_PER_STEP);  // own copies of kt+1 landed, reads of cur done
+#ifdef PHX_CLOCK_PROBE
+    const uint64_t pw1 = __builtin_amdgcn_s_memtime();
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    probe_wait += pw1 - pw0;
+#endif
     __builtin_amdgcn_s_barrier();
+#ifdef PHX_CLOCK_PROBE
+    const uint64_t pw2 = __builtin_amdgcn_s_memtime();
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    probe_bar += pw2 - pw1;
+#endif
     __builtin_amdgcn_sched_barrier(0);
     read_frags(F0, nxt, 0, wm, wn, lane);
     dma_step(cur, A, lda, B, ldb, K, m0, n0, (kt + NSTG) * BK, voa, vob0, vob1, wave);
@@ -396,7 +418,14 @@ extern "C" __global__ __launch_bounds__(NT, 1) void gemm(PHX_MEMREF2(TIn, a, int
     __shared__ __attribute__((aligned(16))) char stg0[STAGE_BYTES];
     __shared__ __attribute__((aligned(16))) char stg1[STAGE_BYTES];
     __shared__ __attribute__((aligned(16))) char stg2[STAGE_BYTES];
+#if NSTG == 4
+    __shared__ __attribute__((aligned(16))) char stg3[STAGE_BYTES];
+    char *const S[NSTG] = {stg0, stg1, stg2, stg3};
+#elif NSTG == 3
     char *const S[NSTG] = {stg0, stg1, stg2};
+#else
+#error "NSTG must be 3 or 4"
+#endif
 #endif
 
     const int64_t M = a_s0, K = a_s1, N = b_s1;
@@ -432,6 +461,12 @@ extern "C" __global__ __launch_bounds__(NT, 1) void gemm(PHX_MEMREF2(TIn, a, int
         (uint32_t)(((lane >> 5) * ldb + 8 * ((lane & 31) ^ (4 * (2 + (lane >> 5))))) * 2);
 #endif
 
+#ifdef PHX_CLOCK_PROBE
+    const uint64_t probe_t0 = __builtin_amdgcn_s_memtime();
+    const uint64_t probe_r0 = __builtin_amdgcn_s_memrealtime();
+    uint32_t probe_m0 = ~0u, probe_n0 = 0;
+    uint64_t probe_wait = 0, probe_bar = 0;
+#endif
     for (uint32_t t = phx_block_linear(); t < ntiles; t += nblk) {
         const uint32_t ts = nblk == ntiles ? phx_xcd_swizzle(t, ntiles) : t;
         const uint32_t gsz = GROUP_M * tiles_n;
@@ -440,6 +475,10 @@ extern "C" __global__ __launch_bounds__(NT, 1) void gemm(PHX_MEMREF2(TIn, a, int
         const uint32_t tm = g0 + (ts % gsz) % gm;
         const uint32_t tn = (ts % gsz) / gm;
         const uint32_t m0 = tm * BM, n0 = tn * BN;
+#ifdef PHX_CLOCK_PROBE
+        probe_m0 = m0;
+        probe_n0 = n0;
+#endif
 
         phx_f16v acc[4][4];
 #pragma unroll
@@ -487,17 +526,31 @@ extern "C" __global__ __launch_bounds__(NT, 1) void gemm(PHX_MEMREF2(TIn, a, int
 #pragma unroll
             for (int u = 0; u < NSTG; ++u)
                 dma_k_step(acc, F0, F1, S[u], S[(u + 1) % NSTG], A, lda, B, ldb, K, m0, n0, kt + u,
-                           voa, vob0, vob1, wm, wn, wave, lane);
+                           voa, vob0, vob1, wm, wn, wave, lane PHX_PROBE_ARGS);
         }
 #pragma unroll
         for (int u = 0; u < NSTG - 1; ++u)
             if (kt + u < nk)
                 dma_k_step(acc, F0, F1, S[u], S[(u + 1) % NSTG], A, lda, B, ldb, K, m0, n0, kt + u,
-                           voa, vob0, vob1, wm, wn, wave, lane);
+                           voa, vob0, vob1, wm, wn, wave, lane PHX_PROBE_ARGS);
         PHX_WAIT_VMCNT(0);
         __syncthreads();
         epilogue(acc, (float *)stg0, C, ldc, m0, n0, wm, wn, alpha, beta, wave, lane);
         __syncthreads();
 #endif
     }
+#ifdef PHX_CLOCK_PROBE
+    // measurement-only build: overwrite two outputs with this workgroup's
+    // shader-clock and 100 MHz real-time spans
+    const uint64_t probe_t1 = __builtin_amdgcn_s_memtime();
+    const uint64_t probe_r1 = __builtin_amdgcn_s_memrealtime();
+    if (tid == 0 && probe_m0 != ~0u) {  // first two outputs of this workgroup's last tile
+        C[(int64_t)probe_m0 * ldc + probe_n0] = (TOut)((float)(probe_t1 - probe_t0) / 64);
+        C[(int64_t)probe_m0 * ldc + probe_n0 + 1] = (TOut)((float)(probe_r1 - probe_r0) / 64);
+    }
+    if (lane == 0 && probe_m0 != ~0u) {  // per wave: cycles in the vm/lds wait and in the barrier
+        C[(int64_t)(probe_m0 + 1 + wave) * ldc + probe_n0] = (TOut)((float)probe_wait / 64);
+        C[(int64_t)(probe_m0 + 1 + wave) * ldc + probe_n0 + 1] = (TOut)((float)probe_bar / 64);
+    }
+#endif
 }

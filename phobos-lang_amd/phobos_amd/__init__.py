@@ -179,7 +179,8 @@ def init(device=0):
     """cust::quick_init (main.rs:169): select the device and load code objects lazily."""
     global _INIT
     if not _INIT:
-        check(lib().phx_init(device, LIB_DIR.encode()))
+        code_dir = os.environ.get("PHX_CODE_OBJECT_DIR") or LIB_DIR
+        check(lib().phx_init(device, code_dir.encode()))
         _INIT = True
 
 
