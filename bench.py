@@ -59,6 +59,9 @@ def parse():
     ap.add_argument("--no-cluster", action="store_true",
                     help="skip the one-pod matmul_cluster job (16384^3 f32 from 3 GiB of files)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--hold", type=float, default=0.0,
+                    help="only launch the --kernels back to back for this many seconds and print "
+                         "the launch count (a steady load for reading power and clocks with amd-smi)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 3 device-to-device copies of 256 MiB (the plain copy the "
                          "FETCH_SIZE/WRITE_SIZE counters are scaled by) and exit")
@@ -270,6 +273,19 @@ def main():
     wanted = all_names if args.kernels == "all" else args.kernels.split(",")
     stream = px.Stream()
     ks = setup(px, stream, wanted)
+    if args.hold > 0:
+        t0, n = time.perf_counter(), 0
+        while time.perf_counter() - t0 < args.hold:
+            for k in ks:
+                for _ in range(REPS[k.name]):
+                    k.launch()
+            stream.synchronize()
+            n += 1
+        dt = time.perf_counter() - t0
+        print(json.dumps({"hold_s": round(dt, 2), "rounds": n,
+                          "kernels": [k.name for k in ks],
+                          "us_per_round": round(dt / n * 1e6, 1)}))
+        return
     ev = [px.Event() for _ in range(len(ks) + 1)]
     # per-step events: ev[i] before kernel i, ev[-1] after the last
     for _ in range(args.warmup):

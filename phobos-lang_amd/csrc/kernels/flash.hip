@@ -22,25 +22,34 @@
 // tensors and runs every head in one launch (grid.y = heads).
 //
 // MI355X design (f16)
-//   * 128 queries per workgroup, 4 waves x 32 queries, 64 keys per step, D=64.
+//   * 256 queries per workgroup, 8 waves x 32 queries, 64 keys per step,
+//     D = 64; two workgroups per CU, so four waves per SIMD.
 //   * Each wave computes S^T = K . Q^T with v_mfma_f32_32x32x16_f16 (K from
 //     LDS is the A operand, Q^T lives in 16 VGPRs as the B operand), so a lane
-//     holds 32 scores of ONE query; the row max/sum is a register reduction
-//     plus one swap with lane^32.
+//     holds 32 scores of ONE query; the row sum is a register reduction plus
+//     one swap with lane^32, and the row max is only taken when needed.
 //   * O^T = V^T . P^T: P^T is the B operand straight from the score registers
-//     (cvt to f16, no LDS round trip); V^T comes from LDS, staged transposed
-//     with bits 2 and 3 of the key index swapped so each lane's 8 keys are
-//     one ds_read_b128.  The per-query rescale is then a per-lane scalar.
-//   * K and V^T are double-buffered in LDS (2 x 16 KiB), next block's global
-//     loads in flight during the current block's 16 MFMAs per wave.
+//     (cvt to f16, no LDS round trip); V^T comes from LDS through the
+//     transposing ds_read_b64_tr_b16.  The per-query rescale is then a
+//     per-lane scalar.
+//   * K and V reach LDS by direct global->LDS copies into a 4-stage ring.
 //   * Workgroups are renumbered XCD-major so all blocks of one head share an
 //     XCD and its L2.
+//   * Measured on MI355X: at these shapes the card runs at its 1.4 kW power
+//     limit (socket power 1346 W, shader clock ~1.8 GHz instead of 2.4), so
+//     the time per head is set by the energy per block.  Staggered and
+//     software-pipelined schedules with two waves per SIMD ran no faster than
+//     this plain four-waves-per-SIMD form.
 #include "phx_common.h"
 
 #define BR PHX_FA_BR
 #define BC PHX_FA_BC
 #define D PHX_FA_D
+#ifdef PHX_FLASH_F16
+#define NT PHX_FA16_THREADS
+#else
 #define NT PHX_FA_THREADS
+#endif
 
 #define LOG2E 1.4426950408889634f
 
@@ -54,10 +63,11 @@ typedef float T;
 #define ROW_BYTES (D * 4)  // 256 bytes
 #endif
 #define TILE_BYTES (BC * ROW_BYTES)  // BC == D == 64 rows
+// second __launch_bounds__ operand: waves per SIMD the register budget must allow
 #ifdef PHX_FLASH_F16
-#define FA_MIN_BLOCKS 2  // two workgroups per CU
+#define FA_WAVES_PER_SIMD 4  // two 8-wave workgroups per CU: <= 128 registers per wave
 #else
-#define FA_MIN_BLOCKS 1
+#define FA_WAVES_PER_SIMD 1
 #endif
 
 // LDS serves 64 banks x 4 bytes per clock on gfx950, so a 16-lane group of a
@@ -88,24 +98,26 @@ __device__ __forceinline__ float xor32_add(float x) {
 
 #ifdef PHX_FLASH_F16
 // ---------------------------------------------------------------- f16 path
-// 256 queries per workgroup: 4 waves x 64 queries (two 32-query halves h),
-// two workgroups per CU (a wave stays under 256 registers), so each SIMD runs
-// two waves whose softmax (VALU) and matrix work (MFMA) overlap.  Per 64-key
-// block a wave runs 32 MFMAs (S^T for both halves: 16; O^T += V^T.P^T for
-// both halves: 16) on 16 KiB of K/V operands read from LDS, half the LDS
-// traffic per flop of a 32-query wave; each run of MFMAs rotates over four
-// independent accumulators.
+// 256 queries per workgroup: 8 waves x 32 queries, two workgroups per CU, so
+// each SIMD holds four waves of at most 128 registers.  A wave's softmax is a
+// chain of dependent VALU ops (fma -> exp -> cvt -> dot2) whose latency one
+// or two waves per SIMD cannot hide; with four, the SIMD always has a wave
+// ready to issue an MFMA while the others run their softmax.  Per 64-key
+// block a wave runs 16 MFMAs (S^T: 8, O^T += V^T.P^T: 8) on 16 KiB of K/V
+// operands read from LDS.
 //
 // K and V blocks are copied global -> LDS directly (buffer_load ... lds, 16
-// bytes per lane) into a ring of 4 stages (K 8 KiB + V 8 KiB each): block
-// i+3 is issued when block i starts, and one barrier per block publishes it.
-#define WQ 64                  // queries per wave
-#define QB (4 * WQ)            // queries per workgroup
+// bytes per lane; each wave copies 8 rows of K and 8 of V) into a ring of 4
+// stages (K 8 KiB + V 8 KiB each): block i+3 is issued when block i starts,
+// and one barrier per block publishes it.
+#define WQ 32                  // queries per wave
+#define NWAVE 8
+#define QB (NWAVE * WQ)        // queries per workgroup
 #define KV_ROW 128             // bytes per K or V row (64 f16)
 #define KV_TILE (BC * KV_ROW)  // 8 KiB
 #define STAGE_BYTES (2 * KV_TILE)
 #define NSTAGE 4
-#define DMA_PER_BLK 4          // copies per wave per key block (2 K + 2 V)
+#define DMA_PER_BLK 2          // copies per wave per key block (K + V)
 
 typedef __fp16 phx_fp16x4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
 typedef __attribute__((address_space(3))) phx_fp16x4 *phx_lds_h4p;
@@ -119,6 +131,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t phx_rsrc(const void *p, uint32
                                              0x00020000);
 }
 
+#define SGB(mask, n) __builtin_amdgcn_sched_group_barrier(mask, n, 0)
+#define G_MFMA 0x008
+#define G_DSR 0x100
+
 // K rows are read as b128 MFMA operands (16 lanes = 16 rows, one chunk):
 // XOR the chunk with (row>>1)&7.  V rows are read with ds_read_b64_tr_b16 (a
 // 32-lane group touches 4 consecutive rows x 64 bytes): rows 2 apart are
@@ -130,62 +146,70 @@ __device__ __forceinline__ uint32_t v_off(uint32_t row, uint32_t chunk) {
     return row * KV_ROW + ((chunk ^ (((row >> 1) & 1) << 2)) << 4);
 }
 
-// Copies key block blk (K and V rows wave*16 .. +15) into stage dst.  Lane l
-// of copy i lands at LDS row wave*16 + 8i + l/8, physical chunk l%8; its
-// source is the logical chunk stored there.  Blocks past the end read an
-// empty buffer (zeros) into a stage that is never consumed.
+// Copies K and V rows wave*8 .. +7 of key block blk into stage dst.  Lane l
+// lands at LDS row wave*8 + l/8, physical chunk l%8; its source (vk, vv) is
+// the logical chunk stored there.  Blocks past the end read an empty buffer
+// (zeros) into a stage that is never consumed.
 __device__ __forceinline__ void dma_block(char *dst, const T *Kp, const T *Vp, int64_t ldk,
-                                          int64_t ldv, uint32_t Nk, uint32_t blk, uint32_t vk0,
-                                          uint32_t vk1, uint32_t vv, uint32_t wave) {
+                                          int64_t ldv, uint32_t Nk, uint32_t blk, uint32_t vk,
+                                          uint32_t vv, uint32_t wave) {
     const bool in = blk * BC < Nk;
     const uint32_t r0 = in ? blk * BC : 0;
     const __amdgpu_buffer_rsrc_t rk =
         phx_rsrc(Kp + (int64_t)r0 * ldk, in ? (uint32_t)(((BC - 1) * ldk + D) * 2) : 0);
     const __amdgpu_buffer_rsrc_t rv =
         phx_rsrc(Vp + (int64_t)r0 * ldv, in ? (uint32_t)(((BC - 1) * ldv + D) * 2) : 0);
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rk, (phx_lds_vp)(dst + (wave * 16 + i * 8) * KV_ROW), 16, i ? vk1 : vk0,
-            (int)((uint32_t)((wave * 16 + i * 8) * ldk) * 2), 0, 0);
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rv, (phx_lds_vp)(dst + KV_TILE + (wave * 16 + i * 8) * KV_ROW), 16, vv,
-            (int)((uint32_t)((wave * 16 + i * 8) * ldv) * 2), 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (phx_lds_vp)(dst + wave * 8 * KV_ROW), 16, vk,
+                                             (int)((uint32_t)(wave * 8 * ldk) * 2), 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (phx_lds_vp)(dst + KV_TILE + wave * 8 * KV_ROW),
+                                             16, vv, (int)((uint32_t)(wave * 8 * ldv) * 2), 0, 0);
 }
 
 // RESCALE_SLACK: the running max is raised only when a row's block max
 // exceeds it by more than 8 (log2 units), so the O/l rescale is skipped on
-// almost every block; p = exp2(s*c - m) then stays <= 2^8, which f16 P and
-// f32 l hold as well as the reference's per-block update.  O = acc / l is
-// the same quantity either way.
+// almost every block; p = exp2(s*c2 - m2) then stays <= 2^8, which f16 P and
+// f32 l hold as well as the reference's per-block update.  O = acc / l is the
+// same quantity either way.
+// Fast path: the row max is not computed on a block unless it is needed.  A
+// lane's 32 p are computed at once with the current m2; when their sum is at
+// most 2^8 no p exceeds 2^8 and the block needs no max.  Otherwise (a
+// wave-uniform branch, rare after the first block) the row max is taken, rows
+// whose max exceeds the slack are raised to it, their p recomputed and acc
+// and l rescaled.  The first key block always takes the max: m2 starts at the
+// first block's row max, as after the reference's first per-block update from
+// m = -65504.
 #define RESCALE_SLACK 8.0f
+#define FAST_SUM_LIMIT 256.0f  // 2^RESCALE_SLACK
 
 struct Flash16 {
-    phx_f16v acc[2][2];  // [half][d tile]: d = 32dt + 8(r/4) + 4g + r%4, query lq
-    float m2[2], l[2];
-    phx_h8 qf[2][4];     // Q^T operand, half h, d slice s: d = 16s + 8g .. +7
+    phx_f16v acc[2];  // [d tile]: d = 32dt + 8(r/4) + 4g + r%4, query lq
+    float m2, l;      // running max (log2 units) and row sum of the lane's query
+    phx_h8 qf[4];     // Q^T operand, d slice s: d = 16s + 8g .. +7
 };
 
-// S^T for both halves: s[h][t] holds keys 32t + 8(r/4) + 4g + r%4 of query
-// 32h + lq.  K operands kf[t][s] = K row 32t + lq, d 16s + 8g .. +7.
-__device__ __forceinline__ void read_k(phx_h8 (&kf)[2][4], const char *Ks, uint32_t lq,
-                                       uint32_t g) {
+// S^T: s[t] holds keys 32t + 8(r/4) + 4g + r%4 of query lq.  K operands:
+// K row 32t + lq, d 16s + 8g .. +7.  Two chains over the d slices.
+__device__ __forceinline__ void scores(phx_f16v (&sc)[2], const char *Ks, const Flash16 &fs,
+                                       uint32_t lq, uint32_t g) {
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int s = 0; s < 4; ++s)
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
-            kf[t][s] = *(const phx_h8 *)(Ks + k_off(32 * t + lq, 2 * s + g));
-}
-
-// MFMA m of the 16: d slice s = m/4 outermost, so consecutive MFMAs update
-// four independent accumulators.
-__device__ __forceinline__ void mfma_s(phx_f16v (&sN)[2][2], const phx_h8 (&kf)[2][4],
-                                       const phx_h8 (&qf)[2][4], int m) {
-    const int s = m >> 2, h = (m >> 1) & 1, t = m & 1;
-    if (s == 0) sN[h][t] = (phx_f16v){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-    sN[h][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[t][s], qf[h][s], sN[h][t], 0, 0, 0);
+        for (int t = 0; t < 2; ++t) {
+            const phx_h8 kf = *(const phx_h8 *)(Ks + k_off(32 * t + lq, 2 * s + g));
+            sc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                kf, fs.qf[s], s ? sc[t] : (phx_f16v){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0},
+                0, 0, 0);
+        }
+    // each K operand is read two MFMAs ahead of its use, not all at once:
+    // the wave has 128 registers
+    SGB(G_DSR, 2);
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+        SGB(G_MFMA, 1);
+        if (m < 6) SGB(G_DSR, 1);
+    }
+    __builtin_amdgcn_sched_barrier(0);
 }
 
 // V^T operand for keys 16c + (4g + 0..3, 8 + 4g + 0..3) (the order P's
@@ -206,10 +230,29 @@ __device__ __forceinline__ phx_h8 read_v(const char *Vs, int c, int dt, uint32_t
     return (phx_h8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
-// exp2(s*c2 - m2) of half h as f16 MFMA operands pf[c] (keys 16c + ...),
-// and the f32 row sum of the f16 values (v_dot2_f32_f16 against (1, 1)).
-__device__ __forceinline__ void softmax_p(phx_h8 (&pf)[4], float &ps, const phx_f16v (&s)[2],
-                                          float c2, float m2) {
+// O^T += V^T . P^T, V^T operands from the stage's V block.
+__device__ __forceinline__ void pv(phx_f16v (&acc)[2], const char *Vs, const phx_h8 (&pf)[4],
+                                   uint32_t lane) {
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt)
+            acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(read_v(Vs, c, dt, lane), pf[c], acc[dt],
+                                                             0, 0, 0);
+    SGB(G_DSR, 4);
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+        SGB(G_MFMA, 1);
+        if (m < 6) SGB(G_DSR, 2);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// exp2(s*c2 - m2) as f16 MFMA operands pf[c] (keys 16c + ...), and the f32
+// sum of the f16 values (v_dot2_f32_f16 against (1, 1)).
+__device__ __forceinline__ float softmax_p(phx_h8 (&pf)[4], const phx_f16v (&s)[2], float c2,
+                                           float m2) {
     const phx_h2 ones = {(_Float16)1.0f, (_Float16)1.0f};
     float part[4];  // one partial sum per key slice: four short dependency chains
 #pragma unroll
@@ -227,11 +270,11 @@ __device__ __forceinline__ void softmax_p(phx_h8 (&pf)[4], float &ps, const phx_
         }
         pf[c] = v;
     }
-    ps = (part[0] + part[1]) + (part[2] + part[3]);
+    return (part[0] + part[1]) + (part[2] + part[3]);
 }
 
-// max over a lane's 32 scores of one half (a running chain, which the
-// compiler turns into v_max3_f32), then across the two lane halves.
+// max over a lane's 32 scores (a running chain, which the compiler turns into
+// v_max3_f32), then across the two lane halves.
 __device__ __forceinline__ float row_max(const phx_f16v (&s)[2]) {
     float m = s[0][0];
 #pragma unroll
@@ -241,129 +284,48 @@ __device__ __forceinline__ float row_max(const phx_f16v (&s)[2]) {
     return xor32_max(m);
 }
 
-// One key block i, in order: scores, row max and lazy rescale, P and its row
-// sums, P.V.  cur = stage of block i, fill = stage that receives block i+3.
-#define SGB(mask, n) __builtin_amdgcn_sched_group_barrier(mask, n, 0)
-#define G_MFMA 0x008
-#define G_VALU 0x002
-#define G_DSR 0x100
-// Softmax of one half.  Each lane (query) raises its own running max, with a
-// select rather than a branch, when its block max exceeds it by more than
-// RESCALE_SLACK; the exps use the new max at once.  The rescale of acc and l
-// (corr = 1 on lanes that did not raise) is applied by fix_half afterwards,
-// behind a wave-uniform branch that is rarely taken.
-__device__ __forceinline__ float half_softmax(phx_h8 (&pf)[4], float &ps, bool &up,
-                                              const phx_f16v (&s)[2], float c2, float m2) {
-    const float mx = row_max(s) * c2;
-    const bool raise = mx > m2 + RESCALE_SLACK;
-    up = raise;
-    const float m2n = raise ? mx : m2;
-    softmax_p(pf, ps, s, c2, m2n);
-    return m2n;
-}
-
-__device__ __forceinline__ void fix_half(Flash16 &fs, int h, bool up, float m2n, float ps) {
-    if (__ballot(up)) {  // wave-uniform
-        const float corr = __builtin_amdgcn_exp2f(fs.m2[h] - m2n);  // 1 where not raised
-        fs.l[h] = fs.l[h] * corr;
-        fs.acc[h][0] = fs.acc[h][0] * corr;
-        fs.acc[h][1] = fs.acc[h][1] * corr;
-        fs.m2[h] = m2n;
-    }
-    fs.l[h] += xor32_add(ps);
-}
-
-// Keeps a half's P and row sum computed inside the region that interleaves
-// them with MFMAs: IR-level code sinking would otherwise move the exps past
-// the rescale branch, out of reach of the instruction scheduler's fences.
-__device__ __forceinline__ void pin_p(phx_h8 (&pf)[4], float &ps) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        phx_u4 u = __builtin_bit_cast(phx_u4, pf[c]);
-        asm volatile("" : "+v"(u));
-        pf[c] = __builtin_bit_cast(phx_h8, u);
-    }
-    asm volatile("" : "+v"(ps));
-}
-
-// One key block i with the two query halves staggered so each half's
-// softmax (VALU) runs under the other half's MFMAs:
-//   A: S_0            B: S_1 || softmax_0
-//   C: O_0 += V.P_0 || softmax_1            D: O_1 += V.P_1
+// One key block i: scores, fast-path P, P.V, and (rarely) the slow path,
+// which recomputes the scores from the K block still in LDS so they need not
+// stay live through P.V.
+template <bool FIRST>
 __device__ __forceinline__ void flash16_step(Flash16 &fs, const char *cur, char *fill,
                                              const T *Kp, const T *Vp, int64_t ldk, int64_t ldv,
-                                             uint32_t Nk, uint32_t i, float c2, uint32_t vk0,
-                                             uint32_t vk1, uint32_t vv, uint32_t wave,
-                                             uint32_t lane) {
+                                             uint32_t Nk, uint32_t i, float c2, uint32_t vk,
+                                             uint32_t vv, uint32_t wave, uint32_t lane) {
     const uint32_t lq = lane & 31, g = lane >> 5;
-    PHX_WAIT_VM_LGKM0(2 * DMA_PER_BLK);  // own copies of block i landed
-    __builtin_amdgcn_s_barrier();          // everyone's block i landed, block i-1 done
+    PHX_WAIT_VM_LGKM0((NSTAGE - 2) * DMA_PER_BLK);  // own copies of block i landed
+    __builtin_amdgcn_s_barrier();                     // everyone's block i landed, i-1 done
     __builtin_amdgcn_sched_barrier(0);
-    dma_block(fill, Kp, Vp, ldk, ldv, Nk, i + 3, vk0, vk1, vv, wave);
-    phx_f16v sc[2][2];
-    phx_h8 kf[2][4];
-    read_k(kf, cur, lq, g);
-    // A: S_0 (two interleaved chains)
+    dma_block(fill, Kp, Vp, ldk, ldv, Nk, i + NSTAGE - 1, vk, vv, wave);
+    phx_f16v sc[2];
+    scores(sc, cur, fs, lq, g);
+    phx_h8 pf[4];
+    float ps = softmax_p(pf, sc, c2, fs.m2);
+    const bool slow = FIRST || __ballot(!(ps <= FAST_SUM_LIMIT));  // wave-uniform; NaN too
+    if (slow) {
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-            sc[0][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                kf[t][s], fs.qf[0][s],
-                s ? sc[0][t] : (phx_f16v){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0}, 0, 0, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    // B: S_1 || softmax_0
-    phx_h8 pf0[4], pf1[4];
-    float ps0, ps1;
-    bool up0, up1;
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-            sc[1][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                kf[t][s], fs.qf[1][s],
-                s ? sc[1][t] : (phx_f16v){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0}, 0, 0, 0);
-    const float m2n0 = half_softmax(pf0, ps0, up0, sc[0], c2, fs.m2[0]);
-#pragma unroll
-    for (int m = 0; m < 8; ++m) {
-        SGB(G_MFMA, 1);
-        SGB(G_VALU, 14);
+        for (int c = 0; c < 4; ++c) pf[c] = (phx_h8){0, 0, 0, 0, 0, 0, 0, 0};
+    } else {
+        fs.l += xor32_add(ps);
     }
-    __builtin_amdgcn_sched_barrier(0);
-    pin_p(pf0, ps0);
-    fix_half(fs, 0, up0, m2n0, ps0);
-    __builtin_amdgcn_sched_barrier(0);
-    // C: O_0 += V_i^T . P_0^T || softmax_1
-    phx_h8 vf[4][2];
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-#pragma unroll
-        for (int dt = 0; dt < 2; ++dt) vf[c][dt] = read_v(cur + KV_TILE, c, dt, lane);
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-#pragma unroll
-        for (int dt = 0; dt < 2; ++dt)
-            fs.acc[0][dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[c][dt], pf0[c], fs.acc[0][dt], 0, 0, 0);
-    const float m2n1 = half_softmax(pf1, ps1, up1, sc[1], c2, fs.m2[1]);
-    SGB(G_DSR, 4);
-    SGB(G_VALU, 16);
-#pragma unroll
-    for (int m = 0; m < 8; ++m) {
-        SGB(G_MFMA, 1);
-        if (m < 6) SGB(G_DSR, 2);
-        SGB(G_VALU, 12);
+    pv(fs.acc, cur + KV_TILE, pf, lane);
+    if (slow) {
+        scores(sc, cur, fs, lq, g);
+        const float mx = row_max(sc) * c2;  // block row max, log2 units
+        const float m2n = (FIRST || mx > fs.m2 + RESCALE_SLACK) ? mx : fs.m2;
+        ps = softmax_p(pf, sc, c2, m2n);
+        if (!FIRST) {
+            const float corr = __builtin_amdgcn_exp2f(fs.m2 - m2n);  // 1 where not raised
+            fs.l = fs.l * corr;
+            fs.acc[0] = fs.acc[0] * corr;
+            fs.acc[1] = fs.acc[1] * corr;
+        }
+        fs.m2 = m2n;
+        fs.l += xor32_add(ps);
+        pv(fs.acc, cur + KV_TILE, pf, lane);
     }
-    __builtin_amdgcn_sched_barrier(0);
-    pin_p(pf1, ps1);
-    fix_half(fs, 1, up1, m2n1, ps1);
-    __builtin_amdgcn_sched_barrier(0);
-    // D: O_1 += V_i^T . P_1^T
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-#pragma unroll
-        for (int dt = 0; dt < 2; ++dt)
-            fs.acc[1][dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[c][dt], pf1[c], fs.acc[1][dt], 0, 0, 0);
 }
+
 __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp, T *O,
                                             int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo,
                                             uint32_t Nq, uint32_t Nk, uint32_t q0, float scale,
@@ -375,55 +337,56 @@ __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp
     const float c2 = scale * LOG2E;
     const uint32_t nkb = Nk / BC;
     char *const S[NSTAGE] = {st0, st1, st2, st3};
+#ifdef PHX_CLOCK_PROBE  // measurement-only build: never built by the Makefile
+    const uint64_t probe_t0 = __builtin_amdgcn_s_memtime();
+    const uint64_t probe_r0 = __builtin_amdgcn_s_memrealtime();
+#endif
 
-    // per-lane source offsets of the LDS copies (see dma_block)
-    const uint32_t vk0 =
-        (uint32_t)(((lane >> 3) * ldk + 8 * ((lane & 7) ^ ((lane >> 4) & 3))) * 2);
-    const uint32_t vk1 =
-        (uint32_t)(((lane >> 3) * ldk + 8 * ((lane & 7) ^ (4 + ((lane >> 4) & 3)))) * 2);
+    // per-lane source offsets of the LDS copies (see dma_block): the K
+    // swizzle depends on bit 2 of the row, i.e. on the wave's parity
+    const uint32_t vk = (uint32_t)(((lane >> 3) * ldk +
+                                    8 * ((lane & 7) ^ (4 * (wave & 1) + ((lane >> 4) & 3)))) * 2);
     const uint32_t vv =
         (uint32_t)(((lane >> 3) * ldv + 8 * ((lane & 7) ^ (((lane >> 4) & 1) << 2))) * 2);
 
 #pragma unroll
-    for (int p = 0; p < 3; ++p) dma_block(S[p], Kp, Vp, ldk, ldv, Nk, p, vk0, vk1, vv, wave);
+    for (int p = 0; p < NSTAGE - 1; ++p) dma_block(S[p], Kp, Vp, ldk, ldv, Nk, p, vk, vv, wave);
 
     Flash16 fs;
     // Q rows past Nq read as zeros (their outputs are not stored)
     const __amdgpu_buffer_rsrc_t rq = phx_rsrc(Q, (uint32_t)(((Nq - 1) * ldq + D) * 2));
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-            fs.qf[h][s] = __builtin_bit_cast(
-                phx_h8, __builtin_amdgcn_raw_buffer_load_b128(
-                            rq, (int)(((qw + 32 * h + lq) * ldq + 16 * s + 8 * g) * 2), 0, 0));
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        fs.acc[h][0] = (phx_f16v){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-        fs.acc[h][1] = fs.acc[h][0];
-        fs.m2[h] = M_INIT * LOG2E;
-        fs.l[h] = 0.0f;
-    }
+    for (int s = 0; s < 4; ++s)
+        fs.qf[s] = __builtin_bit_cast(
+            phx_h8, __builtin_amdgcn_raw_buffer_load_b128(
+                        rq, (int)(((qw + lq) * ldq + 16 * s + 8 * g) * 2), 0, 0));
+    fs.acc[0] = (phx_f16v){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    fs.acc[1] = fs.acc[0];
+    fs.m2 = M_INIT * LOG2E;  // replaced by the first block's row max
+    fs.l = 0.0f;
 
-    uint32_t i = 0;
+    // block b lives in stage b % 4; the copy of block b + 3 goes into stage (b + 3) % 4
+    flash16_step<true>(fs, S[0], S[3], Kp, Vp, ldk, ldv, Nk, 0, c2, vk, vv, wave, lane);
+    uint32_t i = 1;
     for (; i + NSTAGE <= nkb; i += NSTAGE) {
-        flash16_step(fs, S[0], S[3], Kp, Vp, ldk, ldv, Nk, i, c2, vk0, vk1, vv, wave, lane);
-        flash16_step(fs, S[1], S[0], Kp, Vp, ldk, ldv, Nk, i + 1, c2, vk0, vk1, vv, wave, lane);
-        flash16_step(fs, S[2], S[1], Kp, Vp, ldk, ldv, Nk, i + 2, c2, vk0, vk1, vv, wave, lane);
-        flash16_step(fs, S[3], S[2], Kp, Vp, ldk, ldv, Nk, i + 3, c2, vk0, vk1, vv, wave, lane);
+        flash16_step<false>(fs, S[1], S[0], Kp, Vp, ldk, ldv, Nk, i, c2, vk, vv, wave, lane);
+        flash16_step<false>(fs, S[2], S[1], Kp, Vp, ldk, ldv, Nk, i + 1, c2, vk, vv, wave, lane);
+        flash16_step<false>(fs, S[3], S[2], Kp, Vp, ldk, ldv, Nk, i + 2, c2, vk, vv, wave, lane);
+        flash16_step<false>(fs, S[0], S[3], Kp, Vp, ldk, ldv, Nk, i + 3, c2, vk, vv, wave, lane);
     }
-    if (i < nkb) flash16_step(fs, S[0], S[3], Kp, Vp, ldk, ldv, Nk, i, c2, vk0, vk1, vv, wave, lane);
-    if (i + 1 < nkb) flash16_step(fs, S[1], S[0], Kp, Vp, ldk, ldv, Nk, i + 1, c2, vk0, vk1, vv, wave, lane);
-    if (i + 2 < nkb) flash16_step(fs, S[2], S[1], Kp, Vp, ldk, ldv, Nk, i + 2, c2, vk0, vk1, vv, wave, lane);
+    if (i < nkb)
+        flash16_step<false>(fs, S[1], S[0], Kp, Vp, ldk, ldv, Nk, i, c2, vk, vv, wave, lane);
+    if (i + 1 < nkb)
+        flash16_step<false>(fs, S[2], S[1], Kp, Vp, ldk, ldv, Nk, i + 1, c2, vk, vv, wave, lane);
+    if (i + 2 < nkb)
+        flash16_step<false>(fs, S[3], S[2], Kp, Vp, ldk, ldv, Nk, i + 2, c2, vk, vv, wave, lane);
     // drain the copies of the blocks past the end before the LDS is reused
     PHX_WAIT_VMCNT(0);
     __syncthreads();
 
-    // acc[h][dt][r]: d = 32dt + 8(r/4) + 4g + r%4, query qw + 32h + lq.
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const uint32_t q = qw + 32 * h + lq;
-        if (q >= Nq) continue;
+    // acc[dt][r]: d = 32dt + 8(r/4) + 4g + r%4, query qw + lq.
+    const uint32_t q = qw + lq;
+    if (q < Nq) {
         T *orow = O + (int64_t)q * ldo;
 #pragma unroll
         for (int dt = 0; dt < 2; ++dt)
@@ -431,10 +394,19 @@ __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp
             for (int b = 0; b < 4; ++b) {
                 phx_h4 v;
 #pragma unroll
-                for (int rr = 0; rr < 4; ++rr) v[rr] = (_Float16)(fs.acc[h][dt][4 * b + rr] / fs.l[h]);
+                for (int rr = 0; rr < 4; ++rr) v[rr] = (_Float16)(fs.acc[dt][4 * b + rr] / fs.l);
                 *(phx_h4 *)(orow + 32 * dt + 8 * b + 4 * g) = v;
             }
     }
+#ifdef PHX_CLOCK_PROBE
+    // shader-clock and 100 MHz spans of this wave, /64, over O[qw][0..1]
+    const uint64_t probe_t1 = __builtin_amdgcn_s_memtime();
+    const uint64_t probe_r1 = __builtin_amdgcn_s_memrealtime();
+    if (lane == 0 && qw < Nq) {
+        O[(int64_t)qw * ldo] = (_Float16)((float)(probe_t1 - probe_t0) / 64);
+        O[(int64_t)qw * ldo + 1] = (_Float16)((float)(probe_r1 - probe_r0) / 64);
+    }
+#endif
 }
 #else
 // ---------------------------------------------------------------- f32 path
@@ -605,7 +577,7 @@ __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp
     flash_block(Qp, Kp, Vp, Op, ldq, ldk, ldv, ldo, Nk, q0, scale, lds)
 #endif
 
-extern "C" __global__ __launch_bounds__(NT, FA_MIN_BLOCKS) void flash_attention(PHX_MEMREF2(T, q, int64_t),
+extern "C" __global__ __launch_bounds__(NT, FA_WAVES_PER_SIMD) void flash_attention(PHX_MEMREF2(T, q, int64_t),
                                                                   PHX_MEMREF2(T, k, int64_t),
                                                                   PHX_MEMREF2(T, v, int64_t),
                                                                   PHX_MEMREF2(T, o, int64_t),
@@ -622,7 +594,7 @@ extern "C" __global__ __launch_bounds__(NT, FA_MIN_BLOCKS) void flash_attention(
                 o_st0, (uint32_t)Nq, (uint32_t)Nk, rb * FA_QB);
 }
 
-extern "C" __global__ __launch_bounds__(NT, FA_MIN_BLOCKS) void flash_attention_bh(PHX_MEMREF3(T, q, int64_t),
+extern "C" __global__ __launch_bounds__(NT, FA_WAVES_PER_SIMD) void flash_attention_bh(PHX_MEMREF3(T, q, int64_t),
                                                                      PHX_MEMREF3(T, k, int64_t),
                                                                      PHX_MEMREF3(T, v, int64_t),
                                                                      PHX_MEMREF3(T, o, int64_t),

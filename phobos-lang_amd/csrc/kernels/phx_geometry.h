@@ -37,9 +37,10 @@
 
 // flash attention: Nq must be a multiple of PHX_FA_BR; 64 keys per step.
 // f32: 128 query rows per workgroup (4 waves x 32).  f16: 256 query rows per
-// workgroup (4 waves x 64; rows past Nq are computed but not stored).
+// workgroup (8 waves x 32; rows past Nq are computed but not stored).
 #define PHX_FA_BR 128
 #define PHX_FA16_BR 256
 #define PHX_FA_BC 64
 #define PHX_FA_THREADS 256
+#define PHX_FA16_THREADS 512  // f16: 8 waves x 32 queries
 #define PHX_FA_D 64

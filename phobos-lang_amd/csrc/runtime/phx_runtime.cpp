@@ -50,11 +50,11 @@ static const KernelSpec kSpecs[PHX_NUM_KERNELS] = {
     {"gemm_fp16tc_fp32acc.hsaco", "gemm", 64, PHX_H_THREADS},
     {"gemm_fp16.hsaco", "gemm", 64, PHX_H_THREADS},
     {"flash_attention_fp32.hsaco", "flash_attention", 64, PHX_FA_THREADS},
-    {"flash_attention_fp16.hsaco", "flash_attention", 64, PHX_FA_THREADS},
+    {"flash_attention_fp16.hsaco", "flash_attention", 64, PHX_FA16_THREADS},
     {"matmul_cluster_fp32.hsaco", "matmul", 32, PHX_S_THREADS},
     {"matmul_cluster_fp32.hsaco", "matmul_init", 32, PHX_EW_THREADS},
     {"flash_attention_fp32.hsaco", "flash_attention_bh", 64, PHX_FA_THREADS},
-    {"flash_attention_fp16.hsaco", "flash_attention_bh", 64, PHX_FA_THREADS},
+    {"flash_attention_fp16.hsaco", "flash_attention_bh", 64, PHX_FA16_THREADS},
 };
 
 struct State {

@@ -68,7 +68,7 @@ def test_grid_for_and_shape_checks():
     g, b = px.grid_for(px.GEMM_FP32, [384, 640, 32])  # 256-wide tiles, the last ones partial
     assert g == (6, 1, 1)
     g, b = px.grid_for(px.FLASH_FP16_BH, [64, 4096, 4096, 64])
-    assert g == (16, 64, 1) and b == (256, 1, 1)
+    assert g == (16, 64, 1) and b == (512, 1, 1)  # f16: 8 waves x 32 queries
     g, b = px.grid_for(px.FLASH_FP32_BH, [64, 4096, 4096, 64])
     assert g == (32, 64, 1) and b == (256, 1, 1)
     g, b = px.grid_for(px.FLASH_FP16, [384, 1024, 64])  # 256-row workgroups, last one half full

@@ -41,9 +41,9 @@ def _inputs(shape, bits, seed0=1, scale=1.0):
 
 
 @pytest.mark.parametrize("bits", [16, 32])
-# Nk/64 = 1, 3, 5, 6, 7, 16 key blocks covers every tail of the 4-stage copy
+# Nk/64 = 1, 2, 3, 5, 6, 7, 16 key blocks covers every tail of the 4-stage copy
 # ring; Nq = 128, 384, 640 leaves the last 256-row f16 workgroup half full.
-@pytest.mark.parametrize("Nq,Nk", [(128, 64), (256, 192), (128, 320), (128, 384), (640, 448),
+@pytest.mark.parametrize("Nq,Nk", [(128, 64), (128, 128), (256, 192), (128, 320), (128, 384), (640, 448),
                                    (384, 1024)])
 def test_flash_one_head_full(px_gpu, stream, bits, Nq, Nk):
     D = 64
@@ -156,6 +156,7 @@ def test_flash16_bh_any_grid(px_gpu, stream, grid_x):
     px.launch_flash_bh(stream, px.FLASH_FP16_BH, dq.ptr, dk.ptr, dv.ptr, dref.ptr, BH, N, N, D, 0.125)
     fn = px.builtin_function(px.FLASH_FP16_BH)
     px.compute(fn, 64, [(t.ptr, (BH, N, D)) for t in (dq, dk, dv, dgot)],
-               [(4, 4, px.f32_bits(0.125))], (grid_x, 1, 1), (256, 1, 1), stream)
+               [(4, 4, px.f32_bits(0.125))], (grid_x, 1, 1), px.kernel_abi(px.FLASH_FP16_BH)[1],
+               stream)
     stream.synchronize()
     assert np.array_equal(dgot.download(np.uint16, BH * N * D), dref.download(np.uint16, BH * N * D))
