@@ -20,6 +20,7 @@ Prints one JSON line on stdout; progress goes to stderr.
 import argparse
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -59,6 +60,19 @@ def parse():
     ap.add_argument("--no-cluster", action="store_true",
                     help="skip the one-pod matmul_cluster job (16384^3 f32 from 3 GiB of files)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--csv", nargs="?", const="phobos-bench.csv", default=None, metavar="PATH",
+                    help="also write the reference's results CSV (benchmark,impl,precision,gflops,"
+                         "peak_gflops,pct_of_peak; default path phobos-bench.csv)")
+    ap.add_argument("--peak-fp32", type=float, default=None, metavar="TFLOPS",
+                    help="override the f32 peak of the CSV (default: MI355X 157.3)")
+    ap.add_argument("--peak-fp16tc", type=float, default=None, metavar="TFLOPS",
+                    help="override the f16 matrix peak of the CSV (default: MI355X 2516.6)")
+    ap.add_argument("--peak-fp16tcf32acc", type=float, default=None, metavar="TFLOPS",
+                    help="override the f16/f32-accumulate matrix peak of the CSV (default 2516.6)")
+    ap.add_argument("--vendor", action="store_true",
+                    help="add the vendor-library rows of the CSV (the reference's cuBLAS rows): "
+                         "saxpy, sgemm and hgemm through torch on ROCm")
+    ap.add_argument("--vendor-only", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--hold", type=float, default=0.0,
                     help="only launch the --kernels back to back for this many seconds and print "
                          "the launch count (a steady load for reading power and clocks with amd-smi)")
@@ -242,6 +256,88 @@ def cluster_leg(px):
             "ops": {k: stats[k] for k in ("alloc", "load", "compute", "store", "free")}}
 
 
+# CSV rows (phobos-bench/src/main.rs): benchmark name, precision label and
+# GFLOP per launch.  saxpy counts 2 flops per element (main.rs:1284), the GEMMs
+# 2MNK + MN (main.rs:591, 824), flash 4 Nq Nk D per head (main.rs:1032, 1160).
+CSV_ROWS = {
+    "saxpy_fp32": ("saxpy_fp32", "f32", 2 * 4096 * 4096 / 1e9),
+    "gemm_fp32": ("gemm_fp32", "f32", GEMM_FLOP / 1e9),
+    "gemm_fp16tc_fp32acc": ("gemm_fp16tc_fp32acc", "f16-tc-f32-acc", GEMM_FLOP / 1e9),
+    "gemm_fp16": ("gemm_fp16", "f16-tc", GEMM_FLOP / 1e9),
+    "flash_fp32": ("flash_fp32", "f32", FLASH_FLOP / 1e9),
+    "flash_fp16": ("flash_fp16tc_fp32acc", "f16-tc-f32-acc", FLASH_FLOP / 1e9),
+}
+
+
+def vendor_rows(wanted, reps=20):
+    """The reference's cuBLAS comparison rows (main.rs:611-622, 837-848,
+    1295-1306) from the ROCm libraries torch calls: saxpy as y += 2.5 x, the f32
+    GEMM (also the baseline row of gemm_fp16tc_fp32acc, as in the reference) and
+    the f16 GEMM, on the BASELINE shapes.  Timed with torch's events over
+    `reps` launches after 5 warmups.  Returns [(benchmark, impl, precision,
+    gflops)]."""
+    import torch
+    lib = str(torch.backends.cuda.preferred_blas_library()).split(".")[-1].lower()
+    blas = "hipBLASLt" if "lt" in lib else "rocBLAS"
+    N = 4096
+    g = torch.Generator(device="cuda").manual_seed(1)
+
+    def timed(fn):
+        for _ in range(5):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps / 1e3  # s
+
+    rows = []
+    if "saxpy_fp32" in wanted:
+        xs = [torch.rand(N * N, device="cuda", generator=g) for _ in range(4)]
+        ys = [torch.rand(N * N, device="cuda", generator=g) for _ in range(4)]
+        it = iter(range(1 << 30))
+
+        def saxpy():
+            i = next(it) % 4
+            ys[i].add_(xs[i], alpha=2.5)
+        rows.append(("saxpy_fp32", "torch", "f32", CSV_ROWS["saxpy_fp32"][2] / timed(saxpy)))
+    if "gemm_fp32" in wanted or "gemm_fp16tc_fp32acc" in wanted:
+        a, b = (torch.randn(N, N, device="cuda", generator=g) for _ in range(2))
+        t = timed(lambda: torch.mm(a, b))
+        for name in ("gemm_fp32", "gemm_fp16tc_fp32acc"):
+            if name in wanted:
+                rows.append((name, blas, "f32", GEMM_FLOP / 1e9 / t))
+    if "gemm_fp16" in wanted:
+        a, b = (torch.randn(N, N, device="cuda", generator=g, dtype=torch.float16)
+                for _ in range(2))
+        rows.append(("gemm_fp16", blas, "f16-tc", GEMM_FLOP / 1e9 / timed(lambda: torch.mm(a, b))))
+    return rows
+
+
+def write_results_csv(args, kern, wanted):
+    from phobos_amd import report
+    res = report.Results()
+    for name, (bench, prec, gflop) in CSV_ROWS.items():
+        if name in kern:
+            res.push(bench, "phobos", prec, gflop / (kern[name]["ms_avg"] / 1e3))
+    if args.vendor:
+        # torch brings its own HIP runtime, which cannot share a process with
+        # the library's: the vendor rows are timed in a child process
+        cp = subprocess.run([sys.executable, os.path.abspath(__file__), "--vendor-only",
+                             "--kernels", ",".join(wanted)], capture_output=True, text=True,
+                            timeout=600)
+        if cp.returncode != 0:
+            raise RuntimeError(f"vendor rows failed: {cp.stderr[-2000:]}")
+        for row in json.loads(cp.stdout.strip().splitlines()[-1]):
+            res.push(*row)
+    peaks = report.Peaks(args.peak_fp32, args.peak_fp16tc, args.peak_fp16tcf32acc)
+    n = res.write_csv(args.csv, peaks)
+    log(f"theoretical peak: {peaks.describe()}")
+    log(f"wrote {n} rows to {args.csv}")
+
+
 def load_traffic():
     p = os.path.join(ROOT, "profiles", "traffic.json")
     if os.path.exists(p):
@@ -256,6 +352,10 @@ def main():
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
               "(this backend has no multi-GPU path)", file=sys.stderr)
         sys.exit(2)
+    if args.vendor_only:
+        wanted = args.kernels.split(",")
+        print(json.dumps(vendor_rows(wanted)), flush=True)
+        return
     import phobos_amd as px
     px.init(0)
     if args.copy_calibration:
@@ -337,6 +437,8 @@ def main():
         log(f"{k.name:22s} avg {avg:8.4f} ms  min {t.min():8.4f} ms  "
             f"{val:10.2f} {k.unit}  ({100 * val / k.peak:5.1f}% of peak)")
 
+    if args.csv:
+        write_results_csv(args, kern, wanted)
     head = "gemm_fp16tc_fp32acc"
     hk = kern.get(head) or next(iter(kern.values()))
     cluster_res = None

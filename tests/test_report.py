@@ -1,0 +1,51 @@
+"""Results CSV and peaks (phobos-bench/src/report.rs) and the plot script."""
+import os
+import subprocess
+import sys
+
+import pytest
+
+from phobos_amd import report
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def test_csv_rows_match_the_reference_format():
+    # the reference's own results.csv rows (results/results.csv:2,7) rebuilt
+    # from their gflops and peak: one decimal, pct = 100 * gflops / peak
+    res = report.Results()
+    res.push("saxpy_fp32", "phobos", "f32", 72.0)
+    res.push("gemm_fp16", "phobos", "f16-tc", 49691.2)
+    peaks = report.Peaks(fp32_tflops=11.2, fp16tc_tflops=89.2)
+    lines = res.to_csv(peaks).splitlines()
+    assert lines[0] == "benchmark,impl,precision,gflops,peak_gflops,pct_of_peak"
+    assert lines[1] == "saxpy_fp32,phobos,f32,72.0,11200.0,0.6"
+    assert lines[2] == "gemm_fp16,phobos,f16-tc,49691.2,89200.0,55.7"
+
+
+def test_mi355x_peaks_and_overrides():
+    p = report.Peaks()
+    assert p.peak("f32") == 157300.0
+    assert p.peak("f16-tc") == p.peak("f16-tc-f32-acc") == 2516600.0
+    q = report.Peaks(fp16tcf32acc_tflops=1000.0)
+    assert q.peak("f16-tc-f32-acc") == 1e6 and q.peak("f16-tc") == 2516600.0
+    assert "(override)" in q.describe()
+    with pytest.raises(ValueError):
+        report.Results().push("x", "phobos", "bf16", 1.0)
+
+
+def test_write_read_and_plot(tmp_path):
+    res = report.Results()
+    res.push("gemm_fp32", "phobos", "f32", 144200.0)
+    res.push("gemm_fp32", "rocBLAS", "f32", 148000.0)
+    res.push("flash_fp16tc_fp32acc", "phobos", "f16-tc-f32-acc", 954220.0)
+    path = tmp_path / "r.csv"
+    assert res.write_csv(path, report.Peaks()) == 3
+    rows = report.read_csv(path)
+    assert [r["impl"] for r in rows] == ["phobos", "rocBLAS", "phobos"]
+    assert rows[2]["pct"] == pytest.approx(37.9)
+    pytest.importorskip("matplotlib")
+    png = tmp_path / "r.png"
+    subprocess.run([sys.executable, os.path.join(ROOT, "phobos-lang_amd", "plot.py"), str(path),
+                    "-o", str(png)], check=True, capture_output=True, timeout=120)
+    assert png.stat().st_size > 1000
