@@ -39,8 +39,10 @@ GEMM_FLOP = 2 * 4096 ** 3 + 4096 ** 2          # main.rs:591
 FLASH_FLOP = 4 * 4096 * 4096 * 64 * 64         # main.rs:1032, x 64 heads
 FLASH_EXPS = 4096 * 4096 * 64                  # one exp per score (secondary bound)
 SAXPY_BYTES = 12 * 4096 * 4096                 # read x, read y, write y
-# back-to-back launches per kernel per step
-REPS = {"saxpy_fp32": 8, "gemm_fp32": 2, "gemm_fp16tc_fp32acc": 2, "gemm_fp16": 2,
+# back-to-back launches per kernel per step, between two HIP events: enough
+# that the few microseconds an event pair adds stay small against the run
+# (saxpy's launch is 32 us, so it runs 32 times)
+REPS = {"saxpy_fp32": 32, "gemm_fp32": 2, "gemm_fp16tc_fp32acc": 2, "gemm_fp16": 2,
         "flash_fp32": 2, "flash_fp16": 2}
 
 
