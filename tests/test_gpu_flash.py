@@ -160,3 +160,27 @@ def test_flash16_bh_any_grid(px_gpu, stream, grid_x):
                stream)
     stream.synchronize()
     assert np.array_equal(dgot.download(np.uint16, BH * N * D), dref.download(np.uint16, BH * N * D))
+
+
+@pytest.mark.parametrize("bits", [16, 32])
+def test_flash_block_sum_over_limit_without_raise(px_gpu, stream, bits):
+    # Key block 0 scores 0, so the running max (log2 units) is 0 after it.
+    # Block 1 scores s*scale*log2e = 4.0 on every key: each p = 16, a lane's
+    # 32 of them sum to 512 > 2^8, which sends the f16 kernel down its slow
+    # path, but the block max (4) is within the slack of 8, so nothing is
+    # raised.  Block 2 scores -4.  Exact answer from the f64 oracle.
+    D, Nq, Nk = 64, 128, 192
+    q = np.zeros((Nq, D), np.float32)
+    q[:, 0] = 1.0
+    k = np.zeros((Nk, D), np.float32)
+    k[64:128, 0] = 22.1875   # 22.1875 * 0.125 * log2(e) = 4.001
+    k[128:, 0] = -22.1875
+    v = _inputs((Nk, D), bits, 51)[2]
+    dq, dk, dv = (_upload(px_gpu, t, bits) for t in (q, k, v))
+    do = px_gpu.DeviceBuffer(Nq * D * 4)
+    kern = px_gpu.FLASH_FP16 if bits == 16 else px_gpu.FLASH_FP32
+    px_gpu.launch_flash(stream, kern, dq.ptr, dk.ptr, dv.ptr, do.ptr, Nq, Nk, D, 0.125)
+    stream.synchronize()
+    got = _download(do, (Nq, D), bits)
+    want = oracle.flash_rows(np.arange(Nq), q, k, v, 0.125)
+    assert _rel(got, want) < TOL[bits]
