@@ -161,6 +161,18 @@ struct ArgPack {
 
 int launch_raw(hipFunction_t f, const uint32_t grid[3], const uint32_t block[3], uint32_t shmem,
                hipStream_t s, void **args) {
+    // The built-in kernels are written for one workgroup size and do nothing
+    // at any other (they check blockDim on entry): reject such a launch here
+    // rather than let it return without output.
+    for (int k = 0; k < PHX_NUM_KERNELS; ++k) {
+        if (!g.fns[k] || g.fns[k] != f) continue;
+        if (block[0] != kSpecs[k].block || block[1] != 1 || block[2] != 1)
+            return set_error(PHX_E_INVALID,
+                             "%s (%s) runs with a workgroup of (%u,1,1) threads, got (%u,%u,%u); "
+                             "see phx_kernel_abi", kSpecs[k].entry, kSpecs[k].file,
+                             kSpecs[k].block, block[0], block[1], block[2]);
+        break;
+    }
     hipError_t e = hipModuleLaunchKernel(f, grid[0], grid[1], grid[2], block[0], block[1],
                                          block[2], shmem, s, args, nullptr);
     if (e != hipSuccess) return hip_error(e, "hipModuleLaunchKernel");

@@ -184,3 +184,17 @@ def test_flash_block_sum_over_limit_without_raise(px_gpu, stream, bits):
     got = _download(do, (Nq, D), bits)
     want = oracle.flash_rows(np.arange(Nq), q, k, v, 0.125)
     assert _rel(got, want) < TOL[bits]
+
+
+def test_launch_with_wrong_workgroup_size_is_rejected(px_gpu, stream):
+    # flash_fp16 runs 512-thread workgroups; a raw launch with the reference's
+    # cta, or any other size, is refused on the host instead of running a
+    # kernel that would return without output.
+    px = px_gpu
+    BH, N, D = 1, 256, 64
+    bufs = [px.DeviceBuffer(BH * N * D * 2) for _ in range(4)]
+    fn = px.builtin_function(px.FLASH_FP16_BH)
+    with pytest.raises(px.PhxError) as e:
+        px.compute(fn, 64, [(b.ptr, (BH, N, D)) for b in bufs], [(4, 4, px.f32_bits(0.125))],
+                   (1, 1, 1), (256, 1, 1), stream)
+    assert e.value.code == px.PHX_E_INVALID and "phx_kernel_abi" in str(e.value)
