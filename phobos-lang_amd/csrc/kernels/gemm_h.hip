@@ -38,8 +38,11 @@
 //   * Software pipeline, one barrier per K step: the MFMAs of slice 0 run
 //     while the slice-1 operands are read; then each wave waits for its own
 //     copies of the next step and for its reads, and passes the barrier; the
-//     MFMAs of slice 1 run while the next step's slice-0 operands are read and
-//     the copy of a later step is issued into the stage just released.
+//     MFMAs of slice 1 run while the next step's slice-0 operands are read.
+//     gemm_fp16 copies global -> LDS directly into a 4-stage ring, step k+3
+//     into the stage of step k-1 (free once step k-1's barrier has passed),
+//     A's copies during the first half and B's during the second (1.5%
+//     faster than a 3-stage ring with all copies in the second half).
 //     Fences (sched_barrier / sched_group_barrier) fix the interleave, so the
 //     single wave per SIMD keeps its matrix pipe fed.
 //   * gemm_fp16tc: f32 operands are loaded into registers two steps ahead
@@ -352,24 +355,16 @@ __device__ __forceinline__ void tc3_step(phx_f16v (&acc)[4][4], Frags &F0, Frags
 // f16 inputs go global -> LDS directly (buffer_load ... lds: lane l of a
 // 64-lane copy writes LDS bytes base + 16l .. +15 from its own global
 // address, so the XOR-swizzled layouts are built by choosing each lane's
-// source) into a ring of NSTG stages, each its own LDS array so the
-// compiler's LDS-DMA tracking tells them apart.  Step t+NSTG is copied into
-// the stage step t used, once every wave is past the barrier that ends its
-// reads.  Copies of K steps past the end read through an empty buffer
-// resource (zeros) into stages nobody reads, which keeps every wait count
-// constant.
-#ifdef PHX_CLOCK_PROBE
-#define PHX_PROBE_PARAMS , uint64_t &probe_wait, uint64_t &probe_bar
-#define PHX_PROBE_ARGS , probe_wait, probe_bar
-#else
-#define PHX_PROBE_PARAMS
-#define PHX_PROBE_ARGS
-#endif
+// source) into a ring of 4 stages, each its own LDS array so the compiler's
+// LDS-DMA tracking tells them apart.  Step t+3 is copied into the stage step
+// t-1 used, once every wave is past the barrier that ends its reads.  Copies
+// of K steps past the end read through an empty buffer resource (zeros) into
+// stages nobody reads, which keeps every wait count constant.
+#define NSTG 4
 #define DMA_PER_STEP 8  // copies per wave per K step (4 A + 4 B)
-#ifndef NSTG
-#define NSTG 3
-#endif
 
+// PARTS: 1 = A's copies, 2 = B's, 3 = both
+template <int PARTS = 3>
 __device__ __forceinline__ void dma_step(char *dst, const TIn *A, int64_t lda, const TIn *B,
                                          int64_t ldb, int64_t K, uint32_t m0, uint32_t n0,
                                          uint32_t k0, uint32_t voa, uint32_t vob0, uint32_t vob1,
@@ -381,54 +376,50 @@ __device__ __forceinline__ void dma_step(char *dst, const TIn *A, int64_t lda, c
         phx_rsrc(B + (int64_t)(in ? k0 : 0) * ldb + n0, in ? (uint32_t)((BK - 1) * ldb + BN) * 2 : 0);
 #pragma unroll
     for (int i = 0; i < 4; ++i)  // A chunks wave*256 + i*64 + lane: row wave*64 + i*16 + lane/4
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            ra, (phx_lds_vp)(dst + (wave * 256 + i * 64) * 16), 16, voa,
-            (int)((uint32_t)((wave * 64 + i * 16) * lda) * 2), 0, 0);
+        if (PARTS & 1)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                ra, (phx_lds_vp)(dst + (wave * 256 + i * 64) * 16), 16, voa,
+                (int)((uint32_t)((wave * 64 + i * 16) * lda) * 2), 0, 0);
 #pragma unroll
     for (int i = 0; i < 4; ++i)  // B chunks wave*256 + i*64 + lane: row wave*8 + 2i + lane/32
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rb, (phx_lds_vp)(dst + A_BYTES + (wave * 256 + i * 64) * 16), 16, (i & 1) ? vob1 : vob0,
-            (int)((uint32_t)((wave * 8 + i * 2) * ldb) * 2), 0, 0);
+        if (PARTS & 2)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rb, (phx_lds_vp)(dst + A_BYTES + (wave * 256 + i * 64) * 16), 16,
+                (i & 1) ? vob1 : vob0, (int)((uint32_t)((wave * 8 + i * 2) * ldb) * 2), 0, 0);
 }
 
-__device__ __forceinline__ void dma_k_step(phx_f16v (&acc)[4][4], Frags &F0, Frags &F1, char *cur,
-                                           const char *nxt, const TIn *A, int64_t lda,
-                                           const TIn *B, int64_t ldb, int64_t K, uint32_t m0,
-                                           uint32_t n0, uint32_t kt, uint32_t voa, uint32_t vob0,
-                                           uint32_t vob1, uint32_t wm, uint32_t wn, uint32_t wave,
-                                           uint32_t lane PHX_PROBE_PARAMS) {
+// Four-stage form: the copies of step kt+3 go into the stage of step kt-1,
+// which is free once step kt-1's barrier has passed, so A's copies ride with
+// the first half's MFMAs and B's with the second half's.
+__device__ __forceinline__ void dma4_k_step(phx_f16v (&acc)[4][4], Frags &F0, Frags &F1,
+                                            const char *cur, const char *nxt, char *fill,
+                                            const TIn *A, int64_t lda, const TIn *B, int64_t ldb,
+                                            int64_t K, uint32_t m0, uint32_t n0, uint32_t kt,
+                                            uint32_t voa, uint32_t vob0, uint32_t vob1,
+                                            uint32_t wm, uint32_t wn, uint32_t wave,
+                                            uint32_t lane) {
     read_frags(F1, cur, 1, wm, wn, lane);
+    dma_step<1>(fill, A, lda, B, ldb, K, m0, n0, (kt + 3) * BK, voa, vob0, vob1, wave);
     mfma_all(acc, F0);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         SGB(G_MFMA, 1);
         if (i < 12) SGB(G_DSR, 1);
+        if ((i & 3) == 1) SGB(G_VMEM, 1);
     }
     __builtin_amdgcn_sched_barrier(0);
-#ifdef PHX_CLOCK_PROBE
-    const uint64_t pw0 = __builtin_amdgcn_s_memtime();
-#endif
-    PHX_WAIT_VM_LGKM0((NSTG - 2) * DMA_PER_STEP);  // own copies of kt+1 landed, reads of cur done
-#ifdef PHX_CLOCK_PROBE
-    const uint64_t pw1 = __builtin_amdgcn_s_memtime();
-    __builtin_amdgcn_s_waitcnt(0xc07f);
-    probe_wait += pw1 - pw0;
-#endif
+    // own copies of step kt+1 landed: step kt+2 (8) and kt+3's A part (4) may be in flight
+    PHX_WAIT_VM_LGKM0(DMA_PER_STEP + DMA_PER_STEP / 2);
     __builtin_amdgcn_s_barrier();
-#ifdef PHX_CLOCK_PROBE
-    const uint64_t pw2 = __builtin_amdgcn_s_memtime();
-    __builtin_amdgcn_s_waitcnt(0xc07f);
-    probe_bar += pw2 - pw1;
-#endif
     __builtin_amdgcn_sched_barrier(0);
     read_frags(F0, nxt, 0, wm, wn, lane);
-    dma_step(cur, A, lda, B, ldb, K, m0, n0, (kt + NSTG) * BK, voa, vob0, vob1, wave);
+    dma_step<2>(fill, A, lda, B, ldb, K, m0, n0, (kt + 3) * BK, voa, vob0, vob1, wave);
     mfma_all(acc, F1);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         SGB(G_MFMA, 1);
         if (i < 12) SGB(G_DSR, 1);
-        if (i < 8) SGB(G_VMEM, 1);
+        if ((i & 3) == 1) SGB(G_VMEM, 1);
     }
     __builtin_amdgcn_sched_barrier(0);
 }
@@ -445,14 +436,8 @@ extern "C" __global__ __launch_bounds__(NT, 1) void gemm(PHX_MEMREF2(TIn, a, int
     __shared__ __attribute__((aligned(16))) char stg0[STAGE_BYTES];
     __shared__ __attribute__((aligned(16))) char stg1[STAGE_BYTES];
     __shared__ __attribute__((aligned(16))) char stg2[STAGE_BYTES];
-#if NSTG == 4
     __shared__ __attribute__((aligned(16))) char stg3[STAGE_BYTES];
     char *const S[NSTG] = {stg0, stg1, stg2, stg3};
-#elif NSTG == 3
-    char *const S[NSTG] = {stg0, stg1, stg2};
-#else
-#error "NSTG must be 3 or 4"
-#endif
 #endif
 
     const int64_t M = a_s0, K = a_s1, N = b_s1;
@@ -492,7 +477,6 @@ extern "C" __global__ __launch_bounds__(NT, 1) void gemm(PHX_MEMREF2(TIn, a, int
     const uint64_t probe_t0 = __builtin_amdgcn_s_memtime();
     const uint64_t probe_r0 = __builtin_amdgcn_s_memrealtime();
     uint32_t probe_m0 = ~0u, probe_n0 = 0;
-    uint64_t probe_wait = 0, probe_bar = 0;
 #endif
     for (uint32_t t = phx_block_linear(); t < ntiles; t += nblk) {
         const uint32_t ts = nblk == ntiles ? phx_xcd_swizzle(t, ntiles) : t;
@@ -552,23 +536,23 @@ extern "C" __global__ __launch_bounds__(NT, 1) void gemm(PHX_MEMREF2(TIn, a, int
         __syncthreads();
 #else
 #pragma unroll
-        for (int p = 0; p < NSTG; ++p)  // prologue: steps 0 .. NSTG-1 in flight
+        for (int p = 0; p < 3; ++p)  // prologue: steps 0 .. 2 in flight
             dma_step(S[p], A, lda, B, ldb, K, m0, n0, p * BK, voa, vob0, vob1, wave);
-        PHX_WAIT_VMCNT((NSTG - 1) * DMA_PER_STEP);
+        PHX_WAIT_VMCNT(2 * DMA_PER_STEP);
         __builtin_amdgcn_s_barrier();
         read_frags(F0, stg0, 0, wm, wn, lane);
         uint32_t kt = 0;
-        for (; kt + NSTG <= nk; kt += NSTG) {
+        for (; kt + 4 <= nk; kt += 4) {
 #pragma unroll
-            for (int u = 0; u < NSTG; ++u)
-                dma_k_step(acc, F0, F1, S[u], S[(u + 1) % NSTG], A, lda, B, ldb, K, m0, n0, kt + u,
-                           voa, vob0, vob1, wm, wn, wave, lane PHX_PROBE_ARGS);
+            for (int u = 0; u < 4; ++u)
+                dma4_k_step(acc, F0, F1, S[u], S[(u + 1) % 4], S[(u + 3) % 4], A, lda, B, ldb, K,
+                            m0, n0, kt + u, voa, vob0, vob1, wm, wn, wave, lane);
         }
 #pragma unroll
-        for (int u = 0; u < NSTG - 1; ++u)
+        for (int u = 0; u < 3; ++u)
             if (kt + u < nk)
-                dma_k_step(acc, F0, F1, S[u], S[(u + 1) % NSTG], A, lda, B, ldb, K, m0, n0, kt + u,
-                           voa, vob0, vob1, wm, wn, wave, lane PHX_PROBE_ARGS);
+                dma4_k_step(acc, F0, F1, S[u], S[(u + 1) % 4], S[(u + 3) % 4], A, lda, B, ldb, K,
+                            m0, n0, kt + u, voa, vob0, vob1, wm, wn, wave, lane);
         PHX_WAIT_VMCNT(0);
         __syncthreads();
         epilogue(acc, (float *)stg0, C, ldc, m0, n0, wm, wn, alpha, beta, wave, lane);
@@ -583,10 +567,6 @@ extern "C" __global__ __launch_bounds__(NT, 1) void gemm(PHX_MEMREF2(TIn, a, int
     if (tid == 0 && probe_m0 != ~0u) {  // first two outputs of this workgroup's last tile
         C[(int64_t)probe_m0 * ldc + probe_n0] = (TOut)((float)(probe_t1 - probe_t0) / 64);
         C[(int64_t)probe_m0 * ldc + probe_n0 + 1] = (TOut)((float)(probe_r1 - probe_r0) / 64);
-    }
-    if (lane == 0 && probe_m0 != ~0u) {  // per wave: cycles in the vm/lds wait and in the barrier
-        C[(int64_t)(probe_m0 + 1 + wave) * ldc + probe_n0] = (TOut)((float)probe_wait / 64);
-        C[(int64_t)(probe_m0 + 1 + wave) * ldc + probe_n0 + 1] = (TOut)((float)probe_bar / 64);
     }
 #endif
 }
