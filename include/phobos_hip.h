@@ -207,7 +207,7 @@ int phx_f16_to_f32(size_t n, const uint16_t *in, float *out);
 /* One-pod executor for ALLOC/LOAD/COMPUTE/STORE/FREE segments
  * (Engine, phobos-pod/src/engine.rs:121-232, 355-398, 424-509).  The segment
  * is given in the text form documented in INTEGRATION.md; kernels are the
- * built-in ids.  LOAD/STORE use file:// f32 tensors (storage.rs:22-79) staged
+ * built-in ids or functions bound with phx_pod_set_kernel_function.  LOAD/STORE use file:// f32 tensors (storage.rs:22-79) staged
  * through pinned host buffers with async copies. */
 typedef struct phx_pod_s *phx_pod;
 int phx_pod_create(phx_pod *p, size_t arena_bytes, int nstreams);
@@ -217,6 +217,13 @@ int phx_pod_set_tensor(phx_pod p, uint32_t tensor, const char *uri, const uint64
                        uint32_t rank);
 /* Binds a segment kernel id to a built-in kernel (SetKernels). */
 int phx_pod_set_kernel(phx_pod p, uint32_t kernel_id, phx_kernel k);
+/* Binds a segment kernel id to any loaded kernel (phx_module_load_data /
+ * phx_module_get_function), in place of the PTX text a SetKernels or
+ * GetKernel reply carries (phobos-pod/src/server.rs:189-225,
+ * ptx_cache.rs:12-82).  Its COMPUTEs run with the instruction's own grid and
+ * cta, and their tiles are marshalled with index_bits (32 or 64) wide
+ * sizes and strides, as engine.rs:582-647 launches every kernel. */
+int phx_pod_set_kernel_function(phx_pod p, uint32_t kernel_id, phx_function f, int index_bits);
 /* Runs one segment to completion.  stats (nullable) receives
  * {n_alloc, n_load, n_compute, n_store, n_free, compute_ns, wall_ns, io_ns}. */
 int phx_pod_run_segment(phx_pod p, const char *segment_text, uint64_t stats[8]);

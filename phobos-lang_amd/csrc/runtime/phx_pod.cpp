@@ -165,6 +165,9 @@ struct phx_pod_s {
     size_t next_stream = 0;
     std::unordered_map<uint32_t, TensorInfo> tensors;
     std::unordered_map<uint32_t, phx_kernel> kernels;
+    // kernels loaded from code objects the caller supplies (SetKernels with a
+    // gfx950 code object in place of PTX): function and index width
+    std::unordered_map<uint32_t, std::pair<hipFunction_t, int>> functions;
     std::unordered_map<uint64_t, TileBuf> tiles;
     // pinned staging slabs, keyed by byte size
     std::multimap<size_t, void *> pinned_free;
@@ -798,7 +801,18 @@ int phx_pod_set_kernel(phx_pod p, uint32_t kernel_id, phx_kernel k) {
     if (!p || (int)k < 0 || k >= PHX_NUM_KERNELS) return set_error(PHX_E_INVALID, "set_kernel");
     hipFunction_t f;
     if (int rc = builtin(k, &f)) return rc;
+    p->functions.erase(kernel_id);
     p->kernels[kernel_id] = k;
+    return PHX_OK;
+}
+
+int phx_pod_set_kernel_function(phx_pod p, uint32_t kernel_id, phx_function f,
+                                int index_bits) {
+    if (!p || !f) return set_error(PHX_E_INVALID, "set_kernel_function: null pod or function");
+    if (index_bits != 32 && index_bits != 64)
+        return set_error(PHX_E_INVALID, "index_bits must be 32 or 64");
+    p->kernels.erase(kernel_id);
+    p->functions[kernel_id] = {(hipFunction_t)f, index_bits};
     return PHX_OK;
 }
 
@@ -1059,9 +1073,9 @@ static int run_instrs(phx_pod p, std::vector<Instr> &ins, uint64_t stats[8]) {
         }
         case OpKind::Compute: {
             auto kit = p->kernels.find(I.kernel);
-            if (kit == p->kernels.end())
+            auto fit = p->functions.find(I.kernel);
+            if (kit == p->kernels.end() && fit == p->functions.end())
                 return set_error(PHX_E_SEGMENT, "kernel id %u not bound", I.kernel);
-            const phx_kernel k = kit->second;
             std::vector<phx_tile_arg> targs;
             for (auto &a : I.args) {
                 TileBuf *tb;
@@ -1074,31 +1088,39 @@ static int run_instrs(phx_pod p, std::vector<Instr> &ins, uint64_t stats[8]) {
                 for (uint32_t d = 0; d < ta.rank; ++d) ta.shape[d] = tb->shape[d];
                 targs.push_back(ta);
             }
-            // grid from phx_grid_for for the built-in leaves
+            // A caller-supplied kernel runs with the instruction's grid and
+            // cta, as the reference launches every COMPUTE (engine.rs:632-647);
+            // the built-in leaves take theirs from phx_grid_for.
             uint32_t grid[3] = {I.grid[0], I.grid[1], I.grid[2]};
-            uint32_t block[3];
+            uint32_t block[3] = {I.cta[0], I.cta[1], I.cta[2]};
             int bits;
-            kernel_abi(k, &bits, block);
-            int64_t dims[4];
-            int nd = 0;
-            if ((k == PHX_MATMUL || k == PHX_GEMM_FP32) && targs.size() == 3) {
-                dims[0] = (int64_t)targs[0].shape[0];
-                dims[1] = (int64_t)targs[1].shape[1];
-                dims[2] = (int64_t)targs[0].shape[1];
-                nd = 3;
-            } else if (k == PHX_MATMUL_INIT && targs.size() == 1 && targs[0].rank == 2) {
-                dims[0] = (int64_t)targs[0].shape[0];
-                dims[1] = (int64_t)targs[0].shape[1];
-                nd = 2;
-            } else if (k == PHX_SAXPY_FP32 && targs.size() == 3) {
-                dims[0] = (int64_t)targs[0].shape[0];
-                nd = 1;
-            }
-            if (nd) {
-                if (int rc = grid_for(k, dims, nd, grid, block)) return rc;
-            }
             hipFunction_t f;
-            if (int rc = builtin(k, &f)) return rc;
+            if (kit == p->kernels.end()) {
+                f = fit->second.first;
+                bits = fit->second.second;
+            } else {
+                const phx_kernel k = kit->second;
+                kernel_abi(k, &bits, block);
+                int64_t dims[4];
+                int nd = 0;
+                if ((k == PHX_MATMUL || k == PHX_GEMM_FP32) && targs.size() == 3) {
+                    dims[0] = (int64_t)targs[0].shape[0];
+                    dims[1] = (int64_t)targs[1].shape[1];
+                    dims[2] = (int64_t)targs[0].shape[1];
+                    nd = 3;
+                } else if (k == PHX_MATMUL_INIT && targs.size() == 1 && targs[0].rank == 2) {
+                    dims[0] = (int64_t)targs[0].shape[0];
+                    dims[1] = (int64_t)targs[0].shape[1];
+                    nd = 2;
+                } else if (k == PHX_SAXPY_FP32 && targs.size() == 3) {
+                    dims[0] = (int64_t)targs[0].shape[0];
+                    nd = 1;
+                }
+                if (nd) {
+                    if (int rc = grid_for(k, dims, nd, grid, block)) return rc;
+                }
+                if (int rc = builtin(k, &f)) return rc;
+            }
             hipStream_t s = p->streams[p->next_stream];
             p->next_stream = (p->next_stream + 1) % p->streams.size();
             Inflight fl{Inflight::Kernel, i};

@@ -159,6 +159,7 @@ def lib():
     L.phx_pod_set_tensor.argtypes = [_vp, ctypes.c_uint32, ctypes.c_char_p,
                                      ctypes.POINTER(_u64), ctypes.c_uint32]
     L.phx_pod_set_kernel.argtypes = [_vp, ctypes.c_uint32, ctypes.c_int]
+    L.phx_pod_set_kernel_function.argtypes = [_vp, ctypes.c_uint32, _vp, ctypes.c_int]
     L.phx_pod_run_segment.argtypes = [_vp, ctypes.c_char_p, ctypes.POINTER(_u64)]
     L.phx_lcg_fill_f32_stream.argtypes = [ctypes.POINTER(_u64), ctypes.c_size_t, _vp]
     L.phx_pod_set_manifest_pb.argtypes = [_vp, ctypes.c_char_p, ctypes.c_size_t]
@@ -365,6 +366,24 @@ def builtin_function(kernel):
     f = _vp()
     check(lib().phx_builtin_function(ctypes.byref(f), kernel))
     return f.value
+
+
+def module_load_data(image):
+    """PtxCache::insert with a gfx950 code object in place of PTX
+    (phobos-pod/src/ptx_cache.rs:12-82): returns a module handle."""
+    m = _vp()
+    check(lib().phx_module_load_data(ctypes.byref(m), image, len(image)))
+    return m.value
+
+
+def module_get_function(module, name):
+    f = _vp()
+    check(lib().phx_module_get_function(ctypes.byref(f), module, name.encode()))
+    return f.value
+
+
+def module_unload(module):
+    check(lib().phx_module_unload(module))
 
 
 def compute(func, index_bits, tiles, scalars, grid, cta, stream=None):

@@ -281,6 +281,11 @@ class Pod:
     def set_kernel(self, kernel_id, builtin):
         check(lib().phx_pod_set_kernel(self.h, kernel_id, builtin))
 
+    def set_kernel_function(self, kernel_id, function, index_bits=32):
+        """Binds a kernel id to a loaded function (module_load_data /
+        module_get_function); its COMPUTEs use their own grid and cta."""
+        check(lib().phx_pod_set_kernel_function(self.h, kernel_id, function, index_bits))
+
     def run(self, text):
         st = (ctypes.c_uint64 * 8)()
         check(lib().phx_pod_run_segment(self.h, text.encode(), st))

@@ -150,3 +150,44 @@ def test_job_file_runs_on_one_pod(px_gpu, tmp_path):
     r, c = oracle.sample_points(M, N, 64)
     want = oracle.gemm_points(r, c, A, B, C, 0.125, 1.5)
     assert (np.abs(got[r, c] - want) / np.abs(want)).max() < 1e-4
+
+
+def test_loopback_add_from_a_caller_code_object(px_gpu, tmp_path):
+    # The loopback job's second half (phobos-pod/examples/loopback.rs:116-156):
+    # c = a + b over 1024 Lcg draws (seeds 3 and 4), checked bit for bit.  The
+    # `add` leaf is not built in: its code object is loaded from bytes and
+    # bound to the segment's kernel id, as a SetKernels reply binds PTX, and
+    # the COMPUTE runs with its own grid and cta (here the reference-style
+    # 64 x 64 threads).
+    px = px_gpu
+    n = 1024
+    x, y = oracle.lcg_f32(3, n), oracle.lcg_f32(4, n)
+    paths = [str(tmp_path / f) for f in ("a.bin", "b.bin", "c.bin")]
+    x.tofile(paths[0])
+    y.tofile(paths[1])
+    np.zeros(n, np.float32).tofile(paths[2])
+    with open(os.path.join(px.LIB_DIR, "ew_add_fp32.hsaco"), "rb") as f:
+        mod = px.module_load_data(f.read())
+    pod = cl.Pod(64 << 20, nstreams=2)
+    for t, p in enumerate(paths):
+        pod.set_tensor(t, "file://" + p, (n,))
+    seg = "\n".join([
+        "1 - ALLOC 101 1024 f32", "2 - ALLOC 102 1024 f32", "3 - ALLOC 103 1024 f32",
+        "4 1 LOAD 101 0 0 1024", "5 2 LOAD 102 1 0 1024",
+        "6 3,4,5 COMPUTE 9 101:r,102:r,103:w - 64,1,1 64,1,1",
+        "7 6 STORE 103 2 0 1024",
+        "8 7 FREE 101 0", "9 7 FREE 102 0", "10 7 FREE 103 0",
+    ])
+    probe = cl.Pod(64 << 20, nstreams=1)
+    for t, p in enumerate(paths):
+        probe.set_tensor(t, "file://" + p, (n,))
+    with pytest.raises(px.PhxError, match="not bound"):  # kernel id 9 not bound there
+        probe.run(seg)
+    probe.close()
+    pod.set_kernel_function(9, px.module_get_function(mod, "add"), 32)
+    stats = pod.run(seg)
+    assert stats["compute"] == 1 and stats["load"] == 2 and stats["store"] == 1
+    got = np.fromfile(paths[2], np.float32)
+    assert np.array_equal(got.view(np.uint32), (x + y).view(np.uint32))
+    pod.close()
+    px.module_unload(mod)
