@@ -235,8 +235,8 @@ int phx_pod_run_segment(phx_pod p, const char *segment_text, uint64_t stats[8]);
  *     is registered as with phx_pod_set_tensor (f32 file:// tensors); each
  *     KernelEntry is bound by entry-point name to a built-in leaf ("matmul",
  *     "matmul_init", "saxpy"); other names return PHX_E_NOT_FOUND and are
- *     bound by id with phx_pod_set_kernel.  kernel_holders are ignored (no
- *     peer pods).
+ *     bound by id with phx_pod_set_kernel or phx_pod_set_kernel_function.
+ *     kernel_holders are ignored (no peer pods).
  *   phx_pod_run_segment_pb: a phobos.v1.Segment
  *     (phobos-cluster/proto/v1/phobos_v1_isa.proto:107-110), decoded with the
  *     checks of segment_from_proto (phobos-cluster/src/proto.rs:193-275) and
