@@ -67,7 +67,7 @@ typedef float T;
 #ifdef PHX_FLASH_F16
 #define FA_WAVES_PER_SIMD 4  // two 8-wave workgroups per CU: <= 128 registers per wave
 #else
-#define FA_WAVES_PER_SIMD 1
+#define FA_WAVES_PER_SIMD 2  // two 4-wave workgroups per CU: <= 256 registers per wave
 #endif
 
 // LDS serves 64 banks x 4 bytes per clock on gfx950, so a 16-lane group of a
@@ -463,6 +463,8 @@ __device__ __forceinline__ void store_stage(const Stage &st, char *Ks, char *Vt,
     }
 }
 
+#define RESCALE_SLACK 8.0f
+
 __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp, T *O,
                                             int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo,
                                             uint32_t Nk, uint32_t q0, float scale,
@@ -512,23 +514,29 @@ __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp
         for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sT[0][r]);
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sT[1][r]);
-        mx = xor32_max(mx);
-        const float m2new = fmaxf(m2, mx * c2);
-        const float corr = __builtin_amdgcn_exp2f(m2 - m2new);
-        float ps = 0.0f;
+        mx = xor32_max(mx) * c2;
+        // Lazy rescale: the running max is raised only when the block max
+        // exceeds it by more than 8 (log2 units), so p <= 2^8 and O and l are
+        // rescaled only on the rare block that raises some row's max.
+        const bool raise = kb == 0 || mx > m2 + RESCALE_SLACK;
+        const float m2new = raise ? mx : m2;
+        float part[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sT[t][r], c2, -m2new));
-                ps += p;
+                part[r & 3] += p;
                 sT[t][r] = p;
             }
-        ps = xor32_add(ps);
-        l = l * corr + ps;
+        if (__ballot(raise)) {  // wave-uniform
+            const float corr = __builtin_amdgcn_exp2f(m2 - m2new);  // 1 where not raised
+            l = l * corr;
+            acc[0] = acc[0] * corr;
+            acc[1] = acc[1] * corr;
+        }
+        l += xor32_add((part[0] + part[1]) + (part[2] + part[3]));
         m2 = m2new;
-        acc[0] = acc[0] * corr;
-        acc[1] = acc[1] * corr;
         // P^T operand: lane holds keys 32t + 8b + 4g + s = sT[t][4b + s];
         // V^T row d, chunk (8t + 2b + g) holds keys 32t + 8b + 4g .. +3.
 #pragma unroll
