@@ -410,6 +410,14 @@ __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp
 }
 #else
 // ---------------------------------------------------------------- f32 path
+// V^T rows are stored 4 apart by one instruction (the register transpose,
+// rows 4dq + r) and read 16 consecutive at a time (the MFMA operands): XOR
+// the chunk with (row ^ row>>2) & 15, a bijection on both row sets.  With
+// row & 15 the stores hit each bank 4 ways (measured on gfx950: 96.6 vs 73.5
+// cycles per ds_write_b128 in a one-wave loop; reads 61.3 vs 58.2).
+__device__ __forceinline__ uint32_t vt_off(uint32_t row, uint32_t chunk) {
+    return row * ROW_BYTES + ((chunk ^ ((row ^ (row >> 2)) & 15)) << 4);
+}
 // K rows / V^T rows are 64 floats (256 B, 16 chunks).  Waves 0-1 stage V^T
 // via 4x4 register transposes, waves 2-3 stage K; 8 x 16-byte loads each.
 struct Stage {
@@ -448,10 +456,10 @@ __device__ __forceinline__ void store_stage(const Stage &st, char *Ks, char *Vt,
             phx_f4 c1 = {b[0].y, b[1].y, b[2].y, b[3].y};
             phx_f4 c2 = {b[0].z, b[1].z, b[2].z, b[3].z};
             phx_f4 c3 = {b[0].w, b[1].w, b[2].w, b[3].w};
-            *(phx_f4 *)(Vt + lds_off(4 * dq + 0, chunk)) = c0;
-            *(phx_f4 *)(Vt + lds_off(4 * dq + 1, chunk)) = c1;
-            *(phx_f4 *)(Vt + lds_off(4 * dq + 2, chunk)) = c2;
-            *(phx_f4 *)(Vt + lds_off(4 * dq + 3, chunk)) = c3;
+            *(phx_f4 *)(Vt + vt_off(4 * dq + 0, chunk)) = c0;
+            *(phx_f4 *)(Vt + vt_off(4 * dq + 1, chunk)) = c1;
+            *(phx_f4 *)(Vt + vt_off(4 * dq + 2, chunk)) = c2;
+            *(phx_f4 *)(Vt + vt_off(4 * dq + 3, chunk)) = c3;
         }
     } else {
         const uint32_t u = tid - 128;
@@ -545,7 +553,7 @@ __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp
             for (int b = 0; b < 4; ++b)
 #pragma unroll
                 for (int dt = 0; dt < 2; ++dt) {
-                    phx_f4 vf = *(const phx_f4 *)(Vt + lds_off(32 * dt + lq, 8 * t + 2 * b + g));
+                    phx_f4 vf = *(const phx_f4 *)(Vt + vt_off(32 * dt + lq, 8 * t + 2 * b + g));
 #pragma unroll
                     for (int s = 0; s < 4; ++s)
                         acc[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[s], sT[t][4 * b + s],
