@@ -96,6 +96,72 @@ __device__ __forceinline__ float xor32_add(float x) {
     return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
 }
 
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t phx_rsrc(const void *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes,
+                                             0x00020000);
+}
+
+// Buffer resource from the first row of key block blk to the end of the K or
+// V matrix: a block's copies only reach its own 64 rows, so rows past Nk (a
+// partial last block) read zero, and a block past the end has no records.
+// (No min over the block's rows: this form keeps the copy schedule of the
+// full-block loop as it was, measured 4% faster than a clamped row count.)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t kv_rsrc(const T *P, int64_t ld, uint32_t Nk,
+                                                          uint32_t blk) {
+    const bool in = blk * BC < Nk;
+    const uint32_t r0 = in ? blk * BC : 0;
+    const uint32_t bytes = (uint32_t)(((Nk - 1 - r0) * ld + D) * sizeof(T));
+    return phx_rsrc(P + (int64_t)r0 * ld, bytes & (0u - (uint32_t)in));  // no branch
+}
+
+// Scores of keys past Nk in a partial last block become -inf (p = 0): the
+// score accumulators start from this bias (0 for a key that exists, -inf
+// past Nk) instead of zero, so the masked scores come straight out of the
+// MFMA chain with no register beyond the accumulators.  A lane's score
+// register r of tile t holds key 32t + 8(r/4) + 4g + r%4 (both precisions'
+// S^T layouts).  kv: keys of the block that exist, 0 < kv <= 64.  A per-lane
+// limit and a bit select keep the compiler from materialising 32 key indices
+// and compare masks, and the empty asm keeps it from hoisting the 32 bias
+// values (loop-invariant when kv is) to the kernel's entry, where they would
+// stay live, and spill, across the whole key loop.
+__device__ __forceinline__ void key_bias(phx_f16v (&sc)[2], uint32_t kv, uint32_t g) {
+    int32_t lim = (int32_t)kv - 4 * (int32_t)g;  // key 32t+8(r/4)+r%4 must be < lim
+    asm volatile("" : "+v"(lim));
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int32_t c = 32 * t + 8 * (r >> 2) + (r & 3);
+            const uint32_t keep = (uint32_t)((c - lim) >> 31);  // all ones when c < lim
+            sc[t][r] = __builtin_bit_cast(float, 0xff800000u & ~keep);
+        }
+}
+
+// The same mask applied to finished scores (the f32 kernel, whose score
+// accumulators start from the MFMA's inline zero on every full block).  A
+// plain select on the element value: a __builtin_bit_cast of a vector
+// element lvalue was compiled as a read of element 0.
+__device__ __forceinline__ void mask_keys(phx_f16v (&sc)[2], uint32_t kv, uint32_t g) {
+    int32_t lim = (int32_t)kv - 4 * (int32_t)g;
+    asm volatile("" : "+v"(lim));
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const float x = sc[t][r];
+            sc[t][r] = 32 * t + 8 * (r >> 2) + (r & 3) < lim ? x : -__builtin_inff();
+        }
+}
+
+// The softmax is evaluated as exp2(s * c2 - m2) with c2 = scale * log2e.  A
+// negative scale is folded into Q (q -> -q, exact), so that c2 > 0 and the
+// row max of s * c2 is c2 times the row max of s; c2 is at least FLT_MIN so
+// a masked key's -inf score never meets a zero factor (scale 0 then gives
+// equal weights, as exp(0 * s) does).
+__device__ __forceinline__ float softmax_c2(float scale) {
+    return fmaxf(fabsf(scale) * LOG2E, 1.17549435e-38f);
+}
+
 #ifdef PHX_FLASH_F16
 // ---------------------------------------------------------------- f16 path
 // 256 queries per workgroup: 8 waves x 32 queries, two workgroups per CU, so
@@ -126,11 +192,6 @@ typedef __attribute__((address_space(3))) void *phx_lds_vp;
 #define PHX_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14))
 #define PHX_WAIT_VM_LGKM0(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (((n) >> 4) << 14))
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t phx_rsrc(const void *p, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes,
-                                             0x00020000);
-}
-
 #define SGB(mask, n) __builtin_amdgcn_sched_group_barrier(mask, n, 0)
 #define G_MFMA 0x008
 #define G_DSR 0x100
@@ -148,17 +209,13 @@ __device__ __forceinline__ uint32_t v_off(uint32_t row, uint32_t chunk) {
 
 // Copies K and V rows wave*8 .. +7 of key block blk into stage dst.  Lane l
 // lands at LDS row wave*8 + l/8, physical chunk l%8; its source (vk, vv) is
-// the logical chunk stored there.  Blocks past the end read an empty buffer
-// (zeros) into a stage that is never consumed.
+// the logical chunk stored there.  Rows past Nk read zeros; blocks past the
+// end read an empty buffer into a stage that is never consumed.
 __device__ __forceinline__ void dma_block(char *dst, const T *Kp, const T *Vp, int64_t ldk,
                                           int64_t ldv, uint32_t Nk, uint32_t blk, uint32_t vk,
                                           uint32_t vv, uint32_t wave) {
-    const bool in = blk * BC < Nk;
-    const uint32_t r0 = in ? blk * BC : 0;
-    const __amdgpu_buffer_rsrc_t rk =
-        phx_rsrc(Kp + (int64_t)r0 * ldk, in ? (uint32_t)(((BC - 1) * ldk + D) * 2) : 0);
-    const __amdgpu_buffer_rsrc_t rv =
-        phx_rsrc(Vp + (int64_t)r0 * ldv, in ? (uint32_t)(((BC - 1) * ldv + D) * 2) : 0);
+    const __amdgpu_buffer_rsrc_t rk = kv_rsrc(Kp, ldk, Nk, blk);
+    const __amdgpu_buffer_rsrc_t rv = kv_rsrc(Vp, ldv, Nk, blk);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (phx_lds_vp)(dst + wave * 8 * KV_ROW), 16, vk,
                                              (int)((uint32_t)(wave * 8 * ldk) * 2), 0, 0);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (phx_lds_vp)(dst + KV_TILE + wave * 8 * KV_ROW),
@@ -189,6 +246,8 @@ struct Flash16 {
 
 // S^T: s[t] holds keys 32t + 8(r/4) + 4g + r%4 of query lq.  K operands:
 // K row 32t + lq, d 16s + 8g .. +7.  Two chains over the d slices.
+// BIAS: the chain starts from sc's current contents (key_bias), else from 0.
+template <bool BIAS = false>
 __device__ __forceinline__ void scores(phx_f16v (&sc)[2], const char *Ks, const Flash16 &fs,
                                        uint32_t lq, uint32_t g) {
     __builtin_amdgcn_sched_barrier(0);
@@ -198,8 +257,9 @@ __device__ __forceinline__ void scores(phx_f16v (&sc)[2], const char *Ks, const 
         for (int t = 0; t < 2; ++t) {
             const phx_h8 kf = *(const phx_h8 *)(Ks + k_off(32 * t + lq, 2 * s + g));
             sc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                kf, fs.qf[s], s ? sc[t] : (phx_f16v){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0},
-                0, 0, 0);
+                kf, fs.qf[s],
+                (s || BIAS) ? sc[t] : (phx_f16v){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0}, 0,
+                0, 0);
         }
     // each K operand is read two MFMAs ahead of its use, not all at once:
     // the wave has 128 registers
@@ -310,7 +370,12 @@ __device__ __forceinline__ void flash16_step(Flash16 &fs, const char *cur, char 
     }
     pv(fs.acc, cur + KV_TILE, pf, lane);
     if (slow) {
-        scores(sc, cur, fs, lq, g);
+        if (FIRST) {  // block 0 may be partial (Nk < 64): keys past Nk start from -inf
+            key_bias(sc, Nk < BC ? Nk : BC, g);
+            scores<true>(sc, cur, fs, lq, g);
+        } else {
+            scores(sc, cur, fs, lq, g);
+        }
         const float mx = row_max(sc) * c2;  // block row max, log2 units
         const float m2n = (FIRST || mx > fs.m2 + RESCALE_SLACK) ? mx : fs.m2;
         ps = softmax_p(pf, sc, c2, m2n);
@@ -326,6 +391,33 @@ __device__ __forceinline__ void flash16_step(Flash16 &fs, const char *cur, char 
     }
 }
 
+// The partial last key block after at least one full one (kv < 64 keys
+// exist), outside the pipelined loop so the masking costs the full blocks
+// nothing: scores start from the key bias (-inf past Nk), then the plain
+// per-block update with the row max.  No copies are issued; all earlier ones
+// are drained first.
+__device__ __forceinline__ void flash16_last(Flash16 &fs, const char *cur, uint32_t kv, float c2,
+                                             uint32_t lane) {
+    const uint32_t lq = lane & 31, g = lane >> 5;
+    PHX_WAIT_VMCNT(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    phx_f16v sc[2];
+    key_bias(sc, kv, g);
+    scores<true>(sc, cur, fs, lq, g);
+    const float mx = row_max(sc) * c2;  // finite: key 0 always exists
+    const float m2n = mx > fs.m2 + RESCALE_SLACK ? mx : fs.m2;
+    phx_h8 pf[4];
+    const float ps = softmax_p(pf, sc, c2, m2n);
+    const float corr = __builtin_amdgcn_exp2f(fs.m2 - m2n);
+    fs.l = fs.l * corr;
+    fs.acc[0] = fs.acc[0] * corr;
+    fs.acc[1] = fs.acc[1] * corr;
+    fs.m2 = m2n;
+    fs.l += xor32_add(ps);
+    pv(fs.acc, cur + KV_TILE, pf, lane);
+}
+
 __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp, T *O,
                                             int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo,
                                             uint32_t Nq, uint32_t Nk, uint32_t q0, float scale,
@@ -334,8 +426,8 @@ __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t lq = lane & 31, g = lane >> 5;
     const uint32_t qw = q0 + wave * WQ;  // first query of this wave
-    const float c2 = scale * LOG2E;
-    const uint32_t nkb = Nk / BC;
+    const float c2 = softmax_c2(scale);
+    const uint32_t nkb = (Nk + BC - 1) / BC;
     char *const S[NSTAGE] = {st0, st1, st2, st3};
 #ifdef PHX_CLOCK_PROBE  // measurement-only build: never built by the Makefile
     const uint64_t probe_t0 = __builtin_amdgcn_s_memtime();
@@ -360,26 +452,40 @@ __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp
         fs.qf[s] = __builtin_bit_cast(
             phx_h8, __builtin_amdgcn_raw_buffer_load_b128(
                         rq, (int)(((qw + lq) * ldq + 16 * s + 8 * g) * 2), 0, 0));
+    if (scale < 0.0f) {  // wave-uniform
+#pragma unroll
+        for (int s = 0; s < 4; ++s) fs.qf[s] = -fs.qf[s];
+    }
     fs.acc[0] = (phx_f16v){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
     fs.acc[1] = fs.acc[0];
     fs.m2 = M_INIT * LOG2E;  // replaced by the first block's row max
     fs.l = 0.0f;
 
-    // block b lives in stage b % 4; the copy of block b + 3 goes into stage (b + 3) % 4
+    // block b lives in stage b % 4; the copy of block b + 3 goes into stage (b + 3) % 4.
+    // The full blocks run pipelined; a partial last block (Nk % 64 keys) follows.
+    // Block 0 (the first step, whose scores are masked when Nk < 64) always runs.
+    const uint32_t nfull = Nk / BC;
     flash16_step<true>(fs, S[0], S[3], Kp, Vp, ldk, ldv, Nk, 0, c2, vk, vv, wave, lane);
     uint32_t i = 1;
-    for (; i + NSTAGE <= nkb; i += NSTAGE) {
+    for (; i + NSTAGE <= nfull; i += NSTAGE) {
         flash16_step<false>(fs, S[1], S[0], Kp, Vp, ldk, ldv, Nk, i, c2, vk, vv, wave, lane);
         flash16_step<false>(fs, S[2], S[1], Kp, Vp, ldk, ldv, Nk, i + 1, c2, vk, vv, wave, lane);
         flash16_step<false>(fs, S[3], S[2], Kp, Vp, ldk, ldv, Nk, i + 2, c2, vk, vv, wave, lane);
         flash16_step<false>(fs, S[0], S[3], Kp, Vp, ldk, ldv, Nk, i + 3, c2, vk, vv, wave, lane);
     }
-    if (i < nkb)
+    if (i < nfull)
         flash16_step<false>(fs, S[1], S[0], Kp, Vp, ldk, ldv, Nk, i, c2, vk, vv, wave, lane);
-    if (i + 1 < nkb)
+    if (i + 1 < nfull)
         flash16_step<false>(fs, S[2], S[1], Kp, Vp, ldk, ldv, Nk, i + 1, c2, vk, vv, wave, lane);
-    if (i + 2 < nkb)
+    if (i + 2 < nfull)
         flash16_step<false>(fs, S[3], S[2], Kp, Vp, ldk, ldv, Nk, i + 2, c2, vk, vv, wave, lane);
+    if (nfull > 0 && nfull < nkb) {  // wave-uniform; the stage is a constant in each case
+        const uint32_t kv = Nk - nfull * BC;
+        if (nfull % 4 == 0) flash16_last(fs, S[0], kv, c2, lane);
+        else if (nfull % 4 == 1) flash16_last(fs, S[1], kv, c2, lane);
+        else if (nfull % 4 == 2) flash16_last(fs, S[2], kv, c2, lane);
+        else flash16_last(fs, S[3], kv, c2, lane);
+    }
     // drain the copies of the blocks past the end before the LDS is reused
     PHX_WAIT_VMCNT(0);
     __syncthreads();
@@ -420,12 +526,19 @@ __device__ __forceinline__ uint32_t vt_off(uint32_t row, uint32_t chunk) {
 }
 // K rows / V^T rows are 64 floats (256 B, 16 chunks).  Waves 0-1 stage V^T
 // via 4x4 register transposes, waves 2-3 stage K; 8 x 16-byte loads each.
+// In a partial last block (rows past Nk) every row index is clamped to Nk-1:
+// those rows hold finite copies of the last key, whose scores the block's
+// mask sets to -inf, so they add nothing.  (Global loads: buffer loads with a
+// bounded resource measured 3.5% slower here.)
 struct Stage {
     phx_f4 r[8];
 };
 
-__device__ __forceinline__ void load_stage(Stage &st, const T *Kp, const T *Vp, int64_t ldk,
-                                           int64_t ldv, uint32_t key0, uint32_t tid) {
+template <bool CLAMP>
+__device__ __forceinline__ void load_stage_rows(Stage &st, const T *Kp, const T *Vp, int64_t ldk,
+                                                int64_t ldv, uint32_t Nk, uint32_t key0,
+                                                uint32_t tid) {
+    auto row = [&](uint32_t r) { return CLAMP ? (r < Nk ? r : Nk - 1) : r; };
     if (tid < 128) {
         // two 4x4 blocks: keys 4kq..4kq+3 (kq = v/16 and kq+8), d = 4*(v%16)..
         const uint32_t v = tid, dq = v & 15, kq = v >> 4;
@@ -434,15 +547,22 @@ __device__ __forceinline__ void load_stage(Stage &st, const T *Kp, const T *Vp, 
 #pragma unroll
             for (int i = 0; i < 4; ++i)
                 st.r[4 * h + i] =
-                    *(const phx_f4 *)(Vp + (int64_t)(key0 + 4 * (kq + 8 * h) + i) * ldv + 4 * dq);
+                    *(const phx_f4 *)(Vp + (int64_t)row(key0 + 4 * (kq + 8 * h) + i) * ldv + 4 * dq);
     } else {
         const uint32_t u = tid - 128;  // 64 rows x 16 chunks = 1024 = 128 x 8
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t row = i * 8 + (u >> 4), ch = u & 15;
-            st.r[i] = *(const phx_f4 *)(Kp + (int64_t)(key0 + row) * ldk + 4 * ch);
-        }
+        for (int i = 0; i < 8; ++i)
+            st.r[i] = *(const phx_f4 *)(Kp + (int64_t)row(key0 + i * 8 + (u >> 4)) * ldk + 4 * (u & 15));
     }
+}
+
+__device__ __forceinline__ void load_stage(Stage &st, const T *Kp, const T *Vp, int64_t ldk,
+                                           int64_t ldv, uint32_t Nk, uint32_t blk, uint32_t tid) {
+    const uint32_t key0 = blk * BC;
+    if (key0 + BC <= Nk)  // wave-uniform
+        load_stage_rows<false>(st, Kp, Vp, ldk, ldv, Nk, key0, tid);
+    else
+        load_stage_rows<true>(st, Kp, Vp, ldk, ldv, Nk, key0, tid);
 }
 
 __device__ __forceinline__ void store_stage(const Stage &st, char *Ks, char *Vt, uint32_t tid) {
@@ -475,17 +595,22 @@ __device__ __forceinline__ void store_stage(const Stage &st, char *Ks, char *Vt,
 
 __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp, T *O,
                                             int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo,
-                                            uint32_t Nk, uint32_t q0, float scale,
+                                            uint32_t Nq, uint32_t Nk, uint32_t q0, float scale,
                                             char (*lds)[2][TILE_BYTES]) {
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t lq = lane & 31, g = lane >> 5;
     const uint32_t myq = q0 + wave * 32 + lq;
-    const float c2 = scale * LOG2E;
+    const float c2 = softmax_c2(scale);
 
-    // Q^T operand: MFMA (q', s) uses d = 8q' + 4g + s.
+    // Q^T operand: MFMA (q', s) uses d = 8q' + 4g + s.  Rows past Nq read
+    // zeros (their outputs are not stored).
+    const __amdgpu_buffer_rsrc_t rq = phx_rsrc(Q, (uint32_t)(((Nq - 1) * ldq + D) * 4));
+    const float qsign = scale < 0.0f ? -1.0f : 1.0f;  // exact
     phx_f4 qf[8];
 #pragma unroll
-    for (int qq = 0; qq < 8; ++qq) qf[qq] = *(const phx_f4 *)(Q + (int64_t)myq * ldq + 8 * qq + 4 * g);
+    for (int qq = 0; qq < 8; ++qq)
+        qf[qq] = qsign * __builtin_bit_cast(phx_f4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                        rq, (int)((myq * ldq + 8 * qq + 4 * g) * 4), 0, 0));
 
     phx_f16v acc[2];
     acc[0] = (phx_f16v){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
@@ -493,15 +618,15 @@ __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp
     float m2 = M_INIT * LOG2E;
     float l = 0.0f;
 
-    const uint32_t nkb = Nk / BC;
+    const uint32_t nkb = (Nk + BC - 1) / BC;
     Stage st;
-    load_stage(st, Kp, Vp, ldk, ldv, 0, tid);
+    load_stage(st, Kp, Vp, ldk, ldv, Nk, 0, tid);
     store_stage(st, lds[0][0], lds[0][1], tid);
     __syncthreads();
 
     for (uint32_t kb = 0; kb < nkb; ++kb) {
         const uint32_t cur = kb & 1;
-        if (kb + 1 < nkb) load_stage(st, Kp, Vp, ldk, ldv, (kb + 1) * BC, tid);
+        if (kb + 1 < nkb) load_stage(st, Kp, Vp, ldk, ldv, Nk, kb + 1, tid);
         const char *Ks = lds[cur][0];
         const char *Vt = lds[cur][1];
 
@@ -517,6 +642,8 @@ __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp
                     sT[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[s], qf[qq][s], sT[t], 0, 0, 0);
             }
         }
+        const uint32_t kv = Nk - kb * BC;  // keys of this block that exist (uniform)
+        if (kv < BC) mask_keys(sT, kv, g);  // partial last block only
         float mx = sT[0][0];
 #pragma unroll
         for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sT[0][r]);
@@ -564,6 +691,7 @@ __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp
         __syncthreads();
     }
 
+    if (myq >= Nq) return;
     T *orow = O + (int64_t)myq * ldo;
 #pragma unroll
     for (int dt = 0; dt < 2; ++dt)
@@ -590,7 +718,7 @@ __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp
 #define FA_QB BR
 #define FA_LDS_DECL __shared__ __attribute__((aligned(16))) char lds[2][2][TILE_BYTES];
 #define FA_CALL(Qp, Kp, Vp, Op, ldq, ldk, ldv, ldo, Nq, Nk, q0) \
-    flash_block(Qp, Kp, Vp, Op, ldq, ldk, ldv, ldo, Nk, q0, scale, lds)
+    flash_block(Qp, Kp, Vp, Op, ldq, ldk, ldv, ldo, Nq, Nk, q0, scale, lds)
 #endif
 
 extern "C" __global__ __launch_bounds__(NT, FA_WAVES_PER_SIMD) void flash_attention(PHX_MEMREF2(T, q, int64_t),
@@ -601,8 +729,9 @@ extern "C" __global__ __launch_bounds__(NT, FA_WAVES_PER_SIMD) void flash_attent
     FA_LDS_DECL
     const int64_t Nq = q_s0, Nk = k_s0;
     if (blockDim.x != NT || q_s1 != D || k_s1 != D || v_s1 != D || o_s1 != D || v_s0 != Nk ||
-        o_s0 != Nq || Nq % BR || Nk % BC || Nq <= 0 || Nk <= 0 || q_st1 != 1 || k_st1 != 1 ||
-        v_st1 != 1 || o_st1 != 1)
+        o_s0 != Nq || Nq <= 0 || Nk <= 0 || q_st1 != 1 || k_st1 != 1 || v_st1 != 1 ||
+        o_st1 != 1 || (q_st0 | k_st0 | v_st0 | o_st0) % 8 || Nq * q_st0 * 4 > INT32_MAX ||
+        Nk * (k_st0 > v_st0 ? k_st0 : v_st0) * 4 > INT32_MAX)
         return;
     const uint32_t nrb = (uint32_t)((Nq + FA_QB - 1) / FA_QB);
     for (uint32_t rb = phx_block_linear(); rb < nrb; rb += phx_block_count())
@@ -618,8 +747,10 @@ extern "C" __global__ __launch_bounds__(NT, FA_WAVES_PER_SIMD) void flash_attent
     FA_LDS_DECL
     const int64_t H = q_s0, Nq = q_s1, Nk = k_s1;
     if (blockDim.x != NT || k_s0 != H || v_s0 != H || o_s0 != H || q_s2 != D || k_s2 != D ||
-        v_s2 != D || o_s2 != D || v_s1 != Nk || o_s1 != Nq || Nq % BR || Nk % BC || Nq <= 0 ||
-        Nk <= 0 || H <= 0 || q_st2 != 1 || k_st2 != 1 || v_st2 != 1 || o_st2 != 1)
+        v_s2 != D || o_s2 != D || v_s1 != Nk || o_s1 != Nq || Nq <= 0 || Nk <= 0 || H <= 0 ||
+        q_st2 != 1 || k_st2 != 1 || v_st2 != 1 || o_st2 != 1 ||
+        (q_st1 | k_st1 | v_st1 | o_st1 | q_st0 | k_st0 | v_st0 | o_st0) % 8 ||
+        Nq * q_st1 * 4 > INT32_MAX || Nk * (k_st1 > v_st1 ? k_st1 : v_st1) * 4 > INT32_MAX)
         return;
     const uint32_t nrb = (uint32_t)((Nq + FA_QB - 1) / FA_QB);
     const uint32_t nwork = nrb * (uint32_t)H;

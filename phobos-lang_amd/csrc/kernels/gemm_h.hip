@@ -54,6 +54,14 @@
 //   * Workgroups are renumbered XCD-major and grouped 4 tile-rows deep, so the
 //     32 workgroups of one XCD cover a 4x8 block of tiles and share A/B
 //     panels in that XCD's L2.
+//   * Ragged shapes (M any; N a multiple of one 16-byte chunk, 4 f32 or 8
+//     f16 elements; K a multiple of 8, the k extent of a lane's chunk, so
+//     the partial last K step masks whole chunks): each step's buffer resources end at the last row and
+//     column that exist, so rows of A past M and rows of B past K read zeros
+//     (the range check covers the scalar offset too); A chunks past K in the
+//     last, partial K step take an out-of-range lane offset and read zeros;
+//     stores are masked to M x N.  B columns past N in a row are read but
+//     only reach output columns that are not stored.
 #include "phx_common.h"
 
 #ifdef PHX_GEMM_TC
@@ -146,13 +154,33 @@ __device__ __forceinline__ void mfma_all(phx_f16v (&acc)[4][4], const Frags &f) 
 }
 
 // Epilogue: per wave, 8 passes of 16 rows x 128 columns through a private
-// LDS region; a lane then moves 4 consecutive values of a row.
+// LDS region; a lane then moves 4 consecutive values of a row.  C is written
+// (and, for beta != 0, read) through a buffer resource over the tile's rows
+// that exist, so stores to rows past M fall out of range and are dropped; a
+// lane whose 4 columns lie past N gets an out-of-range column offset, fixed
+// for the tile.  No per-store test: an explicit bounds check on every store
+// cost gemm_fp16 5% through its branches and exec-mask updates.  R (ragged)
+// false: the tile lies inside C and stores go through plain pointers.
+template <bool R>
 __device__ __forceinline__ void epilogue(const phx_f16v (&acc)[4][4], float *ep_all, TOut *C,
-                                         int64_t ldc, uint32_t m0, uint32_t n0, uint32_t wm,
-                                         uint32_t wn, float alpha, float beta, uint32_t wave,
-                                         uint32_t lane) {
+                                         int64_t ldc, int64_t M, int64_t N, uint32_t m0,
+                                         uint32_t n0, uint32_t wm, uint32_t wn, float alpha,
+                                         float beta, uint32_t wave, uint32_t lane) {
     const uint32_t lrow = lane & 31, lgrp = lane >> 5;
     float *ep = ep_all + wave * (EP_RP * EP_PITCH);
+    const uint32_t ml = (uint32_t)M - m0;
+    const uint32_t rows = ml < BM ? ml : BM;  // rows of the tile that exist
+    const __amdgpu_buffer_rsrc_t rc =
+        phx_rsrc(C + (int64_t)m0 * ldc, rows * (uint32_t)ldc * (uint32_t)sizeof(TOut));
+    // lane part of the offset (row wm + lane/32, its 4 columns); a store adds
+    // the uniform row step in the scalar offset.  The empty asm keeps the
+    // compiler from hoisting per-store offsets out of the tile loop, where
+    // they would stay live (and spill) across the K loop.
+    const uint32_t pitch = (uint32_t)ldc * (uint32_t)sizeof(TOut);
+    const uint32_t col = n0 + wn + (lane & 31) * 4;
+    uint32_t voff = (wm + (lane >> 5)) * pitch +
+                    (col < (uint32_t)N ? col * (uint32_t)sizeof(TOut) : 0x80000000u);
+    asm volatile("" : "+v"(voff));
 #pragma unroll
     for (int pass = 0; pass < WM / EP_RP; ++pass) {
         const int i = (pass * EP_RP) / 32;
@@ -170,18 +198,28 @@ __device__ __forceinline__ void epilogue(const phx_f16v (&acc)[4][4], float *ep_
         for (int rr = 0; rr < EP_RP / 2; ++rr) {
             const uint32_t row = rr * 2 + (lane >> 5), c4 = (lane & 31) * 4;
             const phx_f4 v = *(const phx_f4 *)(ep + row * EP_PITCH + c4);
+            // row of the tile * pitch + column: < 2^31 in range (the host
+            // limits 257 rows of C to 2 GiB); + 2^31 when the column is past N
+            const int so = (int)((pass * EP_RP + rr * 2) * pitch);
             TOut *dst = C + (int64_t)(m0 + wm + pass * EP_RP + row) * ldc + n0 + wn + c4;
 #ifdef PHX_GEMM_TC
             phx_f4 o = v;
             if (beta != 0.0f) {
-                const phx_f4 c = *(const phx_f4 *)dst;
+                const phx_f4 c = R ? __builtin_bit_cast(phx_f4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                                    rc, (int)voff, so, 0))
+                                   : *(const phx_f4 *)dst;
                 o = v + beta * c;
             }
-            *(phx_f4 *)dst = o;
+            if (R)
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(phx_u4, o), rc, (int)voff, so, 0);
+            else
+                *(phx_f4 *)dst = o;
 #else
             float o[4] = {v.x, v.y, v.z, v.w};
             if (beta != 0.0f) {
-                const phx_h4 c = *(const phx_h4 *)dst;
+                const phx_h4 c = R ? __builtin_bit_cast(phx_h4, __builtin_amdgcn_raw_buffer_load_b64(
+                                                                    rc, (int)voff, so, 0))
+                                   : *(const phx_h4 *)dst;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const float cb = beta * (float)c[e];
@@ -191,7 +229,10 @@ __device__ __forceinline__ void epilogue(const phx_f16v (&acc)[4][4], float *ep_
             phx_h4 h;
 #pragma unroll
             for (int e = 0; e < 4; ++e) h[e] = (_Float16)o[e];
-            *(phx_h4 *)dst = h;
+            if (R)
+                __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(phx_u2, h), rc, (int)voff, so, 0);
+            else
+                *(phx_h4 *)dst = h;
 #endif
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -228,24 +269,67 @@ struct Regs {
     Chunk b[4];
 };
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t a_rsrc(const TIn *A, int64_t lda, int64_t K,
-                                                         uint32_t m0, uint32_t k0) {
-    const bool in = (int64_t)k0 < K;
-    return phx_rsrc(A + (int64_t)m0 * lda + (in ? k0 : 0), in ? (uint32_t)((BM - 1) * lda + BK) * ESZ : 0);
+#endif
+
+// Buffer resources of one K step: A rows m0 .. min(M, m0 + BM) - 1 and B
+// columns n0 .. min(N, n0 + BN) - 1, K columns / rows k0 .. min(K, k0 + BK) - 1;
+// steps past K get an empty resource (every access reads zero).
+// (32-bit arithmetic: the host limits the extents so that 256 rows of either
+// operand span less than 2 GiB.  The clamps are unsigned mins behind an
+// in-range test: a signed clamp becomes v_med3_i32, which moves these
+// wave-uniform values, and the resources built from them, into VGPRs.)
+template <bool R>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t a_rsrc(const TIn *A, uint32_t lda, uint32_t M,
+                                                         uint32_t K, uint32_t m0, uint32_t k0) {
+    if (!R) {  // whole tiles: BM rows x BK columns, or nothing past K
+        const bool in = k0 < K;
+        return phx_rsrc(A + (int64_t)m0 * lda + (in ? k0 : 0),
+                        in ? ((BM - 1) * lda + BK) * (uint32_t)sizeof(TIn) : 0u);
+    }
+    const uint32_t kl = K - k0, ml = M - m0;
+    const uint32_t kw = kl < BK ? kl : BK, mr = ml < BM ? ml : BM;
+    // a resource past K has no records; its base is then never dereferenced
+    const uint32_t in = 0u - (uint32_t)(k0 < K);  // all ones in range: no branch
+    return phx_rsrc(A + (int64_t)m0 * lda + k0, ((mr - 1) * lda + kw) * (uint32_t)sizeof(TIn) & in);
 }
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t b_rsrc(const TIn *B, int64_t ldb, int64_t K,
-                                                         uint32_t n0, uint32_t k0) {
-    const bool in = (int64_t)k0 < K;
-    return phx_rsrc(B + (int64_t)(in ? k0 : 0) * ldb + n0, in ? (uint32_t)((BK - 1) * ldb + BN) * ESZ : 0);
+template <bool R>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t b_rsrc(const TIn *B, uint32_t ldb, uint32_t N,
+                                                         uint32_t K, uint32_t n0, uint32_t k0) {
+    if (!R) {
+        const bool in = k0 < K;
+        return phx_rsrc(B + (int64_t)(in ? k0 : 0) * ldb + n0,
+                        in ? ((BK - 1) * ldb + BN) * (uint32_t)sizeof(TIn) : 0u);
+    }
+    const uint32_t kl = K - k0, nl = N - n0;
+    const uint32_t kw = kl < BK ? kl : BK, nc = nl < BN ? nl : BN;
+    const uint32_t in = 0u - (uint32_t)(k0 < K);
+    return phx_rsrc(B + (int64_t)k0 * ldb + n0, ((kw - 1) * ldb + nc) * (uint32_t)sizeof(TIn) & in);
+}
+// A lane's A offset in step k0: its full-step offset vo, or in the last,
+// partial step (K % BK columns left) vo_tail, which is out of range (reads
+// zero) for the lanes whose chunk lies past K.  vo_tail is fixed per kernel.
+template <bool R>
+__device__ __forceinline__ uint32_t a_lane_off(uint32_t vo, uint32_t vo_tail, uint32_t K,
+                                               uint32_t k0) {
+    return !R || k0 + BK <= K ? vo : vo_tail;
+}
+__device__ __forceinline__ uint32_t a_tail_off(uint32_t vo, uint32_t kc, uint32_t K) {
+    const uint32_t kwl = K % BK;
+    return kwl == 0 || kc < kwl ? vo : 0x80000000u;
 }
 
+#ifdef PHX_GEMM_TC
+
+template <bool RG>
 __device__ __forceinline__ void load_regs(Regs &R, const TIn *A, int64_t lda, const TIn *B,
-                                          int64_t ldb, int64_t K, uint32_t m0, uint32_t n0,
-                                          uint32_t k0, uint32_t voa, uint32_t vob) {
-    const __amdgpu_buffer_rsrc_t ra = a_rsrc(A, lda, K, m0, k0);
-    const __amdgpu_buffer_rsrc_t rb = b_rsrc(B, ldb, K, n0, k0);
+                                          int64_t ldb, int64_t M, int64_t N, int64_t K,
+                                          uint32_t m0, uint32_t n0, uint32_t k0, uint32_t voa,
+                                          uint32_t voa_t, uint32_t vob) {
+    const __amdgpu_buffer_rsrc_t ra = a_rsrc<RG>(A, lda, M, K, m0, k0);
+    const __amdgpu_buffer_rsrc_t rb = b_rsrc<RG>(B, ldb, N, K, n0, k0);
+    const uint32_t va = a_lane_off<RG>(voa, voa_t, K, k0);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) R.a[i] = load_chunk(ra, voa, (int)((uint32_t)(i * 64 * lda) * ESZ));
+    for (int i = 0; i < 4; ++i) R.a[i] = load_chunk(ra, va, (int)((uint32_t)(i * 64 * lda) * ESZ));
 #pragma unroll
     for (int i = 0; i < 4; ++i) R.b[i] = load_chunk(rb, vob, (int)((uint32_t)(i * 8 * ldb) * ESZ));
 }
@@ -302,16 +386,18 @@ __device__ constexpr int tc_slot(int m) {
 // then carries half of the loads and conversions next to its 16 MFMAs
 // (A's in the first, B's in the second) instead of all of them landing in
 // the second half, where the queued loads stalled the in-order MFMA issue.
+template <bool RG>
 __device__ __forceinline__ void tc3_step(phx_f16v (&acc)[4][4], Frags &F0, Frags &F1,
                                          const char *cur, const char *nxt, char *fill, Regs &R,
                                          const TIn *A, int64_t lda, const TIn *B, int64_t ldb,
-                                         int64_t K, uint32_t m0, uint32_t n0, uint32_t kt,
-                                         uint32_t voa, uint32_t vob, uint32_t wm, uint32_t wn,
-                                         uint32_t tid, uint32_t lane) {
+                                         int64_t M, int64_t N, int64_t K, uint32_t m0, uint32_t n0,
+                                         uint32_t kt, uint32_t voa, uint32_t voa_t, uint32_t vob,
+                                         uint32_t wm, uint32_t wn, uint32_t tid, uint32_t lane) {
     const uint32_t k4 = (kt + 4) * BK;
     char *As = fill, *Bs = fill + A_BYTES;
     {
-        const __amdgpu_buffer_rsrc_t ra = a_rsrc(A, lda, K, m0, k4);
+        const __amdgpu_buffer_rsrc_t ra = a_rsrc<RG>(A, lda, M, K, m0, k4);
+        const uint32_t va = a_lane_off<RG>(voa, voa_t, K, k4);
 #pragma unroll
         for (int m = 0; m < 16; ++m) {
             mfma_one(acc, F0, m);
@@ -323,7 +409,7 @@ __device__ __forceinline__ void tc3_step(phx_f16v (&acc)[4][4], Frags &F0, Frags
             } else if (sl >= 9) {
                 const int i = sl - 9;
                 *(phx_u4 *)(As + a_off(i * 64 + (tid >> 2), tid & 3)) = pack(R.a[i]);
-                R.a[i] = load_chunk(ra, voa, (int)((uint32_t)(i * 64 * lda) * ESZ));
+                R.a[i] = load_chunk(ra, va, (int)((uint32_t)(i * 64 * lda) * ESZ));
             }
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -332,7 +418,7 @@ __device__ __forceinline__ void tc3_step(phx_f16v (&acc)[4][4], Frags &F0, Frags
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
     {
-        const __amdgpu_buffer_rsrc_t rb = b_rsrc(B, ldb, K, n0, k4);
+        const __amdgpu_buffer_rsrc_t rb = b_rsrc<RG>(B, ldb, N, K, n0, k4);
 #pragma unroll
         for (int m = 0; m < 16; ++m) {
             mfma_one(acc, F1, m);
@@ -364,21 +450,19 @@ __device__ __forceinline__ void tc3_step(phx_f16v (&acc)[4][4], Frags &F0, Frags
 #define DMA_PER_STEP 8  // copies per wave per K step (4 A + 4 B)
 
 // PARTS: 1 = A's copies, 2 = B's, 3 = both
-template <int PARTS = 3>
+template <bool RG, int PARTS = 3>
 __device__ __forceinline__ void dma_step(char *dst, const TIn *A, int64_t lda, const TIn *B,
-                                         int64_t ldb, int64_t K, uint32_t m0, uint32_t n0,
-                                         uint32_t k0, uint32_t voa, uint32_t vob0, uint32_t vob1,
-                                         uint32_t wave) {
-    const bool in = (int64_t)k0 < K;
-    const __amdgpu_buffer_rsrc_t ra =
-        phx_rsrc(A + (int64_t)m0 * lda + (in ? k0 : 0), in ? (uint32_t)((BM - 1) * lda + BK) * 2 : 0);
-    const __amdgpu_buffer_rsrc_t rb =
-        phx_rsrc(B + (int64_t)(in ? k0 : 0) * ldb + n0, in ? (uint32_t)((BK - 1) * ldb + BN) * 2 : 0);
+                                         int64_t ldb, int64_t M, int64_t N, int64_t K, uint32_t m0,
+                                         uint32_t n0, uint32_t k0, uint32_t voa, uint32_t voa_t,
+                                         uint32_t vob0, uint32_t vob1, uint32_t wave) {
+    const __amdgpu_buffer_rsrc_t ra = a_rsrc<RG>(A, lda, M, K, m0, k0);
+    const __amdgpu_buffer_rsrc_t rb = b_rsrc<RG>(B, ldb, N, K, n0, k0);
+    const uint32_t va = a_lane_off<RG>(voa, voa_t, K, k0);
 #pragma unroll
     for (int i = 0; i < 4; ++i)  // A chunks wave*256 + i*64 + lane: row wave*64 + i*16 + lane/4
         if (PARTS & 1)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                ra, (phx_lds_vp)(dst + (wave * 256 + i * 64) * 16), 16, voa,
+                ra, (phx_lds_vp)(dst + (wave * 256 + i * 64) * 16), 16, va,
                 (int)((uint32_t)((wave * 64 + i * 16) * lda) * 2), 0, 0);
 #pragma unroll
     for (int i = 0; i < 4; ++i)  // B chunks wave*256 + i*64 + lane: row wave*8 + 2i + lane/32
@@ -391,15 +475,17 @@ __device__ __forceinline__ void dma_step(char *dst, const TIn *A, int64_t lda, c
 // Four-stage form: the copies of step kt+3 go into the stage of step kt-1,
 // which is free once step kt-1's barrier has passed, so A's copies ride with
 // the first half's MFMAs and B's with the second half's.
+template <bool RG>
 __device__ __forceinline__ void dma4_k_step(phx_f16v (&acc)[4][4], Frags &F0, Frags &F1,
                                             const char *cur, const char *nxt, char *fill,
                                             const TIn *A, int64_t lda, const TIn *B, int64_t ldb,
-                                            int64_t K, uint32_t m0, uint32_t n0, uint32_t kt,
-                                            uint32_t voa, uint32_t vob0, uint32_t vob1,
+                                            int64_t M, int64_t N, int64_t K, uint32_t m0,
+                                            uint32_t n0, uint32_t kt,
+                                            uint32_t voa, uint32_t voa_t, uint32_t vob0, uint32_t vob1,
                                             uint32_t wm, uint32_t wn, uint32_t wave,
                                             uint32_t lane) {
     read_frags(F1, cur, 1, wm, wn, lane);
-    dma_step<1>(fill, A, lda, B, ldb, K, m0, n0, (kt + 3) * BK, voa, vob0, vob1, wave);
+    dma_step<RG, 1>(fill, A, lda, B, ldb, M, N, K, m0, n0, (kt + 3) * BK, voa, voa_t, vob0, vob1, wave);
     mfma_all(acc, F0);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -413,7 +499,7 @@ __device__ __forceinline__ void dma4_k_step(phx_f16v (&acc)[4][4], Frags &F0, Fr
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
     read_frags(F0, nxt, 0, wm, wn, lane);
-    dma_step<2>(fill, A, lda, B, ldb, K, m0, n0, (kt + 3) * BK, voa, vob0, vob1, wave);
+    dma_step<RG, 2>(fill, A, lda, B, ldb, M, N, K, m0, n0, (kt + 3) * BK, voa, voa_t, vob0, vob1, wave);
     mfma_all(acc, F1);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -425,47 +511,45 @@ __device__ __forceinline__ void dma4_k_step(phx_f16v (&acc)[4][4], Frags &F0, Fr
 }
 #endif
 
-extern "C" __global__ __launch_bounds__(NT, 1) void gemm(PHX_MEMREF2(TIn, a, int64_t),
-                                                          PHX_MEMREF2(TIn, b, int64_t),
-                                                          PHX_MEMREF2(TOut, c, int64_t),
-                                                          float alpha, float beta) {
+// The kernel body.  RG (ragged): M, N or K is not a whole number of tiles,
+// so operand resources end at the matrix edges, A chunks past K in the last
+// step read zero and C is stored through a bounded resource; whole-tile
+// shapes run the instance without any of that (the masks cost gemm_fp16tc
+// 2% when always on).
+template <bool RG>
+__device__ __forceinline__ void gemm_body(const TIn *A, const TIn *B, TOut *C, int64_t lda,
+                                          int64_t ldb, int64_t ldc, int64_t M, int64_t N,
+                                          int64_t K, float alpha, float beta,
 #ifdef PHX_GEMM_TC
-    __shared__ __attribute__((aligned(16))) char stg[3 * STAGE_BYTES];
+                                          char *stg
+#else
+                                          char *stg0, char *stg1, char *stg2, char *stg3
+#endif
+) {
+#ifdef PHX_GEMM_TC
     char *const stg0 = stg;  // the epilogue's staging area
 #else
-    __shared__ __attribute__((aligned(16))) char stg0[STAGE_BYTES];
-    __shared__ __attribute__((aligned(16))) char stg1[STAGE_BYTES];
-    __shared__ __attribute__((aligned(16))) char stg2[STAGE_BYTES];
-    __shared__ __attribute__((aligned(16))) char stg3[STAGE_BYTES];
     char *const S[NSTG] = {stg0, stg1, stg2, stg3};
 #endif
-
-    const int64_t M = a_s0, K = a_s1, N = b_s1;
-    if (blockDim.x != NT || M % BM || N % BN || K % BK || M <= 0 || N <= 0 || K <= 0 ||
-        b_s0 != K || c_s0 != M || c_s1 != N || a_st1 != 1 || b_st1 != 1 || c_st1 != 1)
-        return;
-
-    const TIn *A = a_ptr + a_off;
-    const TIn *B = b_ptr + b_off;
-    TOut *C = c_ptr + c_off;
-    const int64_t lda = a_st0, ldb = b_st0, ldc = c_st0;
 
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t wm = (wave >> 1) * WM;
     const uint32_t wn = (wave & 1) * WN;
-    const uint32_t tiles_n = (uint32_t)(N / BN);
-    const uint32_t tiles_m = (uint32_t)(M / BM);
+    const uint32_t tiles_n = (uint32_t)((N + BN - 1) / BN);
+    const uint32_t tiles_m = (uint32_t)((M + BM - 1) / BM);
     const uint32_t ntiles = tiles_m * tiles_n;
     const uint32_t nblk = phx_block_count();
-    const uint32_t nk = (uint32_t)(K / BK);
+    const uint32_t nk = (uint32_t)((K + BK - 1) / BK);
 #ifdef PHX_GEMM_TC
     const uint32_t voa = (uint32_t)(((tid >> 2) * lda + (tid & 3) * 8) * ESZ);
+    const uint32_t voa_t = a_tail_off(voa, (tid & 3) * 8, K);  // 8 k per chunk, K % 8 == 0
     const uint32_t vob = (uint32_t)(((tid >> 5) * ldb + (tid & 31) * 8) * ESZ);
 #else
     const uint32_t voa =
         (uint32_t)(((lane >> 2) * lda + 8 * ((lane & 3) ^ ((lane >> 4) & 3))) * 2);
+    const uint32_t voa_t = a_tail_off(voa, 8 * ((lane & 3) ^ ((lane >> 4) & 3)), K);
     // B row parity within the 4-row swizzle period: 2*(i&1) + lane/32
     const uint32_t vob0 =
         (uint32_t)(((lane >> 5) * ldb + 8 * ((lane & 31) ^ (4 * (lane >> 5)))) * 2);
@@ -503,17 +587,17 @@ extern "C" __global__ __launch_bounds__(NT, 1) void gemm(PHX_MEMREF2(TIn, a, int
         // prologue: steps 0 and 1 into LDS stages 0 and 1, steps 2 and 3 in
         // flight; step t lives in stage t % 3 and register set t % 2
         Regs R0, R1;
-        load_regs(R0, A, lda, B, ldb, K, m0, n0, 0, voa, vob);
-        load_regs(R1, A, lda, B, ldb, K, m0, n0, BK, voa, vob);
+        load_regs<RG>(R0, A, lda, B, ldb, M, N, K, m0, n0, 0, voa, voa_t, vob);
+        load_regs<RG>(R1, A, lda, B, ldb, M, N, K, m0, n0, BK, voa, voa_t, vob);
         store_regs(R0, stg, tid);
         store_regs(R1, stg + STAGE_BYTES, tid);
-        load_regs(R0, A, lda, B, ldb, K, m0, n0, 2 * BK, voa, vob);
-        load_regs(R1, A, lda, B, ldb, K, m0, n0, 3 * BK, voa, vob);
+        load_regs<RG>(R0, A, lda, B, ldb, M, N, K, m0, n0, 2 * BK, voa, voa_t, vob);
+        load_regs<RG>(R1, A, lda, B, ldb, M, N, K, m0, n0, 3 * BK, voa, voa_t, vob);
         PHX_WAIT_VM_LGKM0(63);
         __builtin_amdgcn_s_barrier();
         read_frags(F0, stg, 0, wm, wn, lane);
 #define TC3(cur, nxt, fill, R, t)                                                               \
-        tc3_step(acc, F0, F1, cur, nxt, fill, R, A, lda, B, ldb, K, m0, n0, t, voa, vob, wm, wn, \
+        tc3_step<RG>(acc, F0, F1, cur, nxt, fill, R, A, lda, B, ldb, M, N, K, m0, n0, t, voa, voa_t, vob, wm, wn, \
                  tid, lane)
         // stage bases rotate at run time (uniform values), so the LDS
         // addresses are one per-lane offset plus a scalar base instead of a
@@ -532,12 +616,12 @@ extern "C" __global__ __launch_bounds__(NT, 1) void gemm(PHX_MEMREF2(TIn, a, int
 #undef TC3
         PHX_WAIT_VMCNT(0);
         __syncthreads();
-        epilogue(acc, (float *)stg0, C, ldc, m0, n0, wm, wn, alpha, beta, wave, lane);
+        epilogue<RG>(acc, (float *)stg0, C, ldc, M, N, m0, n0, wm, wn, alpha, beta, wave, lane);
         __syncthreads();
 #else
 #pragma unroll
         for (int p = 0; p < 3; ++p)  // prologue: steps 0 .. 2 in flight
-            dma_step(S[p], A, lda, B, ldb, K, m0, n0, p * BK, voa, vob0, vob1, wave);
+            dma_step<RG>(S[p], A, lda, B, ldb, M, N, K, m0, n0, p * BK, voa, voa_t, vob0, vob1, wave);
         PHX_WAIT_VMCNT(2 * DMA_PER_STEP);
         __builtin_amdgcn_s_barrier();
         read_frags(F0, stg0, 0, wm, wn, lane);
@@ -545,17 +629,17 @@ extern "C" __global__ __launch_bounds__(NT, 1) void gemm(PHX_MEMREF2(TIn, a, int
         for (; kt + 4 <= nk; kt += 4) {
 #pragma unroll
             for (int u = 0; u < 4; ++u)
-                dma4_k_step(acc, F0, F1, S[u], S[(u + 1) % 4], S[(u + 3) % 4], A, lda, B, ldb, K,
-                            m0, n0, kt + u, voa, vob0, vob1, wm, wn, wave, lane);
+                dma4_k_step<RG>(acc, F0, F1, S[u], S[(u + 1) % 4], S[(u + 3) % 4], A, lda, B, ldb, M,
+                            N, K, m0, n0, kt + u, voa, voa_t, vob0, vob1, wm, wn, wave, lane);
         }
 #pragma unroll
         for (int u = 0; u < 3; ++u)
             if (kt + u < nk)
-                dma4_k_step(acc, F0, F1, S[u], S[(u + 1) % 4], S[(u + 3) % 4], A, lda, B, ldb, K,
-                            m0, n0, kt + u, voa, vob0, vob1, wm, wn, wave, lane);
+                dma4_k_step<RG>(acc, F0, F1, S[u], S[(u + 1) % 4], S[(u + 3) % 4], A, lda, B, ldb, M,
+                            N, K, m0, n0, kt + u, voa, voa_t, vob0, vob1, wm, wn, wave, lane);
         PHX_WAIT_VMCNT(0);
         __syncthreads();
-        epilogue(acc, (float *)stg0, C, ldc, m0, n0, wm, wn, alpha, beta, wave, lane);
+        epilogue<RG>(acc, (float *)stg0, C, ldc, M, N, m0, n0, wm, wn, alpha, beta, wave, lane);
         __syncthreads();
 #endif
     }
@@ -569,4 +653,47 @@ extern "C" __global__ __launch_bounds__(NT, 1) void gemm(PHX_MEMREF2(TIn, a, int
         C[(int64_t)probe_m0 * ldc + probe_n0 + 1] = (TOut)((float)(probe_r1 - probe_r0) / 64);
     }
 #endif
+}
+
+extern "C" __global__ __launch_bounds__(NT, 1) void gemm(PHX_MEMREF2(TIn, a, int64_t),
+                                                          PHX_MEMREF2(TIn, b, int64_t),
+                                                          PHX_MEMREF2(TOut, c, int64_t),
+                                                          float alpha, float beta) {
+#ifdef PHX_GEMM_TC
+    __shared__ __attribute__((aligned(16))) char stg[3 * STAGE_BYTES];
+#else
+    __shared__ __attribute__((aligned(16))) char stg0[STAGE_BYTES];
+    __shared__ __attribute__((aligned(16))) char stg1[STAGE_BYTES];
+    __shared__ __attribute__((aligned(16))) char stg2[STAGE_BYTES];
+    __shared__ __attribute__((aligned(16))) char stg3[STAGE_BYTES];
+#endif
+
+    const int64_t M = a_s0, K = a_s1, N = b_s1;
+#ifdef PHX_GEMM_TC
+    constexpr int64_t NMULT = PHX_TC_N_MULT, KMULT = PHX_TC_K_MULT;
+#else
+    constexpr int64_t NMULT = PHX_H16_NK_MULT, KMULT = PHX_H16_NK_MULT;
+#endif
+    if (blockDim.x != NT || N % NMULT || K % KMULT || M <= 0 || N <= 0 || K <= 0 || b_s0 != K ||
+        c_s0 != M || c_s1 != N || a_st1 != 1 || b_st1 != 1 || c_st1 != 1 ||
+        a_st0 % KMULT || (b_st0 | c_st0) % NMULT || M > INT32_MAX ||
+        (BM + 1) * (a_st0 > b_st0 ? a_st0 : b_st0) * (int64_t)sizeof(TIn) > INT32_MAX ||
+        (BM + 1) * c_st0 * (int64_t)sizeof(TOut) > INT32_MAX ||
+        ((uintptr_t)(a_ptr + a_off) | (uintptr_t)(b_ptr + b_off) | (uintptr_t)(c_ptr + c_off)) & 15)
+        return;
+
+    const TIn *A = a_ptr + a_off;
+    const TIn *B = b_ptr + b_off;
+    TOut *C = c_ptr + c_off;
+    const int64_t lda = a_st0, ldb = b_st0, ldc = c_st0;
+#ifdef PHX_GEMM_TC
+#define GEMM_LDS stg
+#else
+#define GEMM_LDS stg0, stg1, stg2, stg3
+#endif
+    if (M % BM == 0 && N % BN == 0 && K % BK == 0)  // uniform
+        gemm_body<false>(A, B, C, lda, ldb, ldc, M, N, K, alpha, beta, GEMM_LDS);
+    else
+        gemm_body<true>(A, B, C, lda, ldb, ldc, M, N, K, alpha, beta, GEMM_LDS);
+#undef GEMM_LDS
 }

@@ -21,8 +21,14 @@
 //     2x2 arrangement, each owning 128x128 = 4x4 v_mfma_f32_32x32x2_f32 tiles
 //     whose 256 accumulators live in AGPRs.  K step 16: 128 MFMAs (8192
 //     matrix-core cycles) per wave per step, so one barrier per step costs
-//     little.  Tiles that cross M or N are computed from zero-filled loads and
-//     stored masked, so M and N only need to be multiples of 128.
+//     little.
+//   * Ragged shapes (M any, N and K multiples of 4, so every 16-byte chunk is
+//     whole): each step's buffer resources end at the last row / column that
+//     exists, so rows past M and B rows past K read zeros (the range check
+//     covers the scalar offset too); A chunks past K in the last, partial K
+//     step take an out-of-range lane offset and read zeros; tiles crossing M
+//     or N are stored masked.  Columns of B past N in a row are read but only
+//     reach output columns that are not stored.
 //   * The MFMA's 2-wide k slice is permuted so that a lane's four consecutive
 //     MFMAs read four consecutive k: lane group g of MFMA s uses k = 8q + 4g +
 //     s.  A is staged As[m][k] (64-byte rows, 16-byte chunks XOR (row>>2)&3),
@@ -122,12 +128,16 @@ __device__ __forceinline__ void mfma_all(phx_f16v (&acc)[4][4], const Frags &f) 
 // chunk its swizzled slot holds.  Rows past M read zeros.
 __device__ __forceinline__ void dma_step(char *dst, const float *A, int64_t lda, const float *B,
                                          int64_t ldb, int64_t M, int64_t N, int64_t K, uint32_t m0,
-                                         uint32_t n0, uint32_t k0, uint32_t voa, uint32_t vob0,
-                                         uint32_t vob1, uint32_t wave) {
+                                         uint32_t n0, uint32_t k0, uint32_t voa, uint32_t voa_t,
+                                         uint32_t vob0, uint32_t vob1, uint32_t wave) {
     const bool in = (int64_t)k0 < K;
     const int64_t mrows = M - m0 < BM ? M - m0 : BM;
+    const int64_t kr = in ? K - k0 : 0;  // columns of this step that exist
+    const int64_t kw = kr < BK ? kr : BK;
     const __amdgpu_buffer_rsrc_t ra = phx_rsrc(
-        A + (int64_t)m0 * lda + (in ? k0 : 0), in ? (uint32_t)(((mrows - 1) * lda + BK) * 4) : 0);
+        A + (int64_t)m0 * lda + (in ? k0 : 0), in ? (uint32_t)(((mrows - 1) * lda + kw) * 4) : 0);
+    // the last, partial step uses the offsets that read zero past K
+    const uint32_t va = kw == BK ? voa : voa_t;
     // B rows are full 1 KiB reads even when the tile crosses N: columns past
     // N land in output columns that are not stored; the resource ends at the
     // matrix's last element.
@@ -138,7 +148,7 @@ __device__ __forceinline__ void dma_step(char *dst, const float *A, int64_t lda,
 #pragma unroll
     for (int i = 0; i < 4; ++i)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            ra, (phx_lds_vp)(dst + (wave * 256 + i * 64) * 16), 16, voa,
+            ra, (phx_lds_vp)(dst + (wave * 256 + i * 64) * 16), 16, va,
             (int)((uint32_t)((wave * 64 + i * 16) * lda) * 4), 0, 0);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -152,7 +162,8 @@ __device__ __forceinline__ void k_step(phx_f16v (&acc)[4][4], Frags &F0, Frags &
                                        const char *nxt, const float *A, int64_t lda,
                                        const float *B, int64_t ldb, int64_t M, int64_t N,
                                        int64_t K, uint32_t m0, uint32_t n0, uint32_t kt,
-                                       uint32_t voa, uint32_t vob0, uint32_t vob1, uint32_t wm,
+                                       uint32_t voa, uint32_t voa_t, uint32_t vob0, uint32_t vob1,
+                                       uint32_t wm,
                                        uint32_t wn, uint32_t wave, uint32_t lane) {
     read_frags(F1, cur, 1, wm, wn, lane);
     mfma_all(acc, F0);
@@ -166,7 +177,7 @@ __device__ __forceinline__ void k_step(phx_f16v (&acc)[4][4], Frags &F0, Frags &
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
     read_frags(F0, nxt, 0, wm, wn, lane);
-    dma_step(cur, A, lda, B, ldb, M, N, K, m0, n0, (kt + NSTG) * BK, voa, vob0, vob1, wave);
+    dma_step(cur, A, lda, B, ldb, M, N, K, m0, n0, (kt + NSTG) * BK, voa, voa_t, vob0, vob1, wave);
     mfma_all(acc, F1);
 #pragma unroll
     for (int i = 0; i < 64; ++i) {
@@ -240,9 +251,14 @@ __device__ __forceinline__ void gemm_s_body(const float *A, int64_t lda, const f
     const uint32_t tiles_m = (uint32_t)((M + BM - 1) / BM);
     const uint32_t ntiles = tiles_m * tiles_n;
     const uint32_t nblk = phx_block_count();
-    const uint32_t nk = (uint32_t)(K / BK);
+    const uint32_t nk = (uint32_t)((K + BK - 1) / BK);
     const uint32_t voa =
         (uint32_t)(((lane >> 2) * lda + 4 * ((lane & 3) ^ ((lane >> 4) & 3))) * 4);
+    // lane's logical A chunk covers k = 4 * ((lane & 3) ^ ((lane >> 4) & 3)) .. +3;
+    // in the last, partial K step chunks past K read zero
+    const uint32_t kwl = (uint32_t)(K % BK);
+    const uint32_t voa_t =
+        kwl == 0 || 4 * ((lane & 3) ^ ((lane >> 4) & 3)) < kwl ? voa : 0x80000000u;
     const uint32_t vob0 = lane * 16;
     const uint32_t vob1 = (lane ^ 8) * 16;
 
@@ -264,7 +280,7 @@ __device__ __forceinline__ void gemm_s_body(const float *A, int64_t lda, const f
         Frags F0, F1;
 #pragma unroll
         for (int p = 0; p < NSTG; ++p)
-            dma_step(S[p], A, lda, B, ldb, M, N, K, m0, n0, p * BK, voa, vob0, vob1, wave);
+            dma_step(S[p], A, lda, B, ldb, M, N, K, m0, n0, p * BK, voa, voa_t, vob0, vob1, wave);
         PHX_WAIT_VMCNT((NSTG - 1) * DMA_PER_STEP);
         __builtin_amdgcn_s_barrier();
         read_frags(F0, stg0, 0, wm, wn, lane);
@@ -273,13 +289,13 @@ __device__ __forceinline__ void gemm_s_body(const float *A, int64_t lda, const f
 #pragma unroll
             for (int u = 0; u < NSTG; ++u)
                 k_step(acc, F0, F1, S[u], S[(u + 1) % NSTG], A, lda, B, ldb, M, N, K, m0, n0,
-                       kt + u, voa, vob0, vob1, wm, wn, wave, lane);
+                       kt + u, voa, voa_t, vob0, vob1, wm, wn, wave, lane);
         }
 #pragma unroll
         for (int u = 0; u < NSTG - 1; ++u)
             if (kt + u < nk)
                 k_step(acc, F0, F1, S[u], S[(u + 1) % NSTG], A, lda, B, ldb, M, N, K, m0, n0,
-                       kt + u, voa, vob0, vob1, wm, wn, wave, lane);
+                       kt + u, voa, voa_t, vob0, vob1, wm, wn, wave, lane);
         PHX_WAIT_VMCNT(0);
         __syncthreads();
         epilogue<STEP>(acc, (float *)stg0, C, ldc, M, N, m0, n0, wm, wn, alpha, beta, wave, lane);
@@ -292,9 +308,10 @@ __device__ __forceinline__ void gemm_s_body(const float *A, int64_t lda, const f
     __shared__ __attribute__((aligned(16))) char stg1[STAGE_BYTES];                           \
     __shared__ __attribute__((aligned(16))) char stg2[STAGE_BYTES];                           \
     const int64_t M = a_s0, K = a_s1, N = b_s1;                                               \
-    if (blockDim.x != NT || M % PHX_S_BM || N % PHX_S_BN || K % PHX_S_BK || M <= 0 ||        \
-        N <= 0 || K <= 0 || b_s0 != K || c_s0 != M || c_s1 != N || a_st1 != 1 || b_st1 != 1 || \
-        c_st1 != 1)                                                                           \
+    if (blockDim.x != NT || N % PHX_S_NK_MULT || K % PHX_S_NK_MULT || M <= 0 || N <= 0 ||  \
+        K <= 0 || b_s0 != K || c_s0 != M || c_s1 != N || a_st1 != 1 || b_st1 != 1 ||         \
+        c_st1 != 1 || (a_st0 | b_st0 | c_st0) % 4 ||                                         \
+        ((uintptr_t)(a_ptr + a_off) | (uintptr_t)(b_ptr + b_off) | (uintptr_t)(c_ptr + c_off)) & 15) \
         return;
 
 #ifdef PHX_GEMM_FP32

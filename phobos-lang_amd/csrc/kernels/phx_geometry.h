@@ -14,30 +14,37 @@
 #endif
 #define PHX_SAXPY_BLOCK_ELEMS (PHX_SAXPY_THREADS * PHX_SAXPY_VEC * 4)
 
+// GEMM shapes: M is any positive extent; N and K must be multiples of the
+// element count of one 16-byte chunk of the operand type (4 for f32 storage,
+// 8 for f16; K % 8 for gemm_fp16tc, whose lanes stage 8 k at a time), so
+// every staged chunk is whole and every row starts 16-byte aligned.  Tiles crossing M, N or K are masked inside the kernels.  (The
+// reference's own tiles need M and N multiples of 32 and K of its K tile.)
+
 // f16-operand GEMMs (gemm_fp16, gemm_fp16tc_fp32acc): 256x256 output tile,
 // K step 32, 256 threads = 4 waves in a 2x2 arrangement of 128x128.
 #define PHX_H_BM 256
 #define PHX_H_BN 256
 #define PHX_H_BK 32
 #define PHX_H_THREADS 256
+#define PHX_TC_N_MULT 4    // gemm_fp16tc_fp32acc (f32 storage): N % 4, K % 8
+#define PHX_TC_K_MULT 8
+#define PHX_H16_NK_MULT 8  // gemm_fp16 (f16 storage): N % 8, K % 8
 
-// f32 GEMM (gemm_fp32, cluster matmul): M and N must be multiples of
-// PHX_S_BM / PHX_S_BN and K of PHX_S_BK; a workgroup computes a
-// PHX_S_TILE x PHX_S_TILE output tile (4 waves of 128x128) and masks the part
-// past M or N.
-#define PHX_S_BM 128
-#define PHX_S_BN 128
+// f32 GEMM (gemm_fp32, cluster matmul): a workgroup computes a
+// PHX_S_TILE x PHX_S_TILE output tile (4 waves of 128x128).
 #define PHX_S_TILE 256
-#define PHX_S_BK 32
 #define PHX_S_THREADS 256
+#define PHX_S_NK_MULT 4
 
 // matmul_init: element-wise, 256 threads x 4 float4.
 #define PHX_EW_THREADS 256
 #define PHX_EW_BLOCK_ELEMS (256 * 16)
 
-// flash attention: Nq must be a multiple of PHX_FA_BR; 64 keys per step.
-// f32: 128 query rows per workgroup (4 waves x 32).  f16: 256 query rows per
-// workgroup (8 waves x 32; rows past Nq are computed but not stored).
+// flash attention: any Nq >= 1 and Nk >= 1, D == 64; 64 keys per step (keys
+// past Nk in the last step are masked out of the softmax).  f32: 128 query
+// rows per workgroup (4 waves x 32).  f16: 256 query rows per workgroup (8
+// waves x 32).  Query rows past Nq are computed from zero queries and not
+// stored.
 #define PHX_FA_BR 128
 #define PHX_FA16_BR 256
 #define PHX_FA_BC 64

@@ -196,26 +196,29 @@ int check_shape(phx_kernel k, const int64_t *d, int nd) {
         return PHX_OK;
     case PHX_GEMM_FP16TC_FP32ACC:
     case PHX_GEMM_FP16:
-        if (int rc = need(3)) return rc;
-        if (d[0] == 0 || d[1] == 0 || d[2] == 0 || d[0] % PHX_H_BM || d[1] % PHX_H_BN ||
-            d[2] % PHX_H_BK)
-            return set_error(PHX_E_INVALID,
-                             "f16 gemm needs M%%%d==0, N%%%d==0, K%%%d==0 (got %lld,%lld,%lld)",
-                             PHX_H_BM, PHX_H_BN, PHX_H_BK, (long long)d[0], (long long)d[1],
-                             (long long)d[2]);
-        return PHX_OK;
     case PHX_GEMM_FP32:
-    case PHX_MATMUL:
+    case PHX_MATMUL: {
         if (int rc = need(3)) return rc;
-        if (d[0] == 0 || d[1] == 0 || d[2] == 0 || d[0] % PHX_S_BM || d[1] % PHX_S_BN ||
-            d[2] % PHX_S_BK)
+        const int nm = k == PHX_GEMM_FP16 ? PHX_H16_NK_MULT
+                       : k == PHX_GEMM_FP16TC_FP32ACC ? PHX_TC_N_MULT
+                                                      : PHX_S_NK_MULT;
+        const int km = k == PHX_GEMM_FP16 ? PHX_H16_NK_MULT
+                       : k == PHX_GEMM_FP16TC_FP32ACC ? PHX_TC_K_MULT
+                                                      : PHX_S_NK_MULT;
+        if (d[0] == 0 || d[1] == 0 || d[2] == 0 || d[1] % nm || d[2] % km)
             return set_error(PHX_E_INVALID,
-                             "f32 gemm needs M%%%d==0, N%%%d==0, K%%%d==0 (got %lld,%lld,%lld)",
-                             PHX_S_BM, PHX_S_BN, PHX_S_BK, (long long)d[0], (long long)d[1],
-                             (long long)d[2]);
-        if (!fits_i32(d[0] * d[2]) || !fits_i32(d[2] * d[1]) || !fits_i32(d[0] * d[1]))
-            return set_error(PHX_E_INVALID, "f32 gemm extents exceed the i32 index");
+                             "gemm needs M>0, N%%%d==0, K%%%d==0 (got %lld,%lld,%lld)", nm, km,
+                             (long long)d[0], (long long)d[1], (long long)d[2]);
+        if (kSpecs[k].index_bits == 32 &&
+            (!fits_i32(d[0] * d[2]) || !fits_i32(d[2] * d[1]) || !fits_i32(d[0] * d[1])))
+            return set_error(PHX_E_INVALID, "gemm extents exceed the i32 index");
+        // per-tile buffer resources span up to 256 rows of a matrix
+        const int64_t esz = k == PHX_GEMM_FP16 ? 2 : 4;
+        if ((PHX_H_BM + 1) * (d[1] > d[2] ? d[1] : d[2]) * esz > INT32_MAX)
+            return set_error(PHX_E_INVALID, "gemm rows too long (N or K = %lld)",
+                             (long long)(d[1] > d[2] ? d[1] : d[2]));
         return PHX_OK;
+    }
     case PHX_MATMUL_INIT:
         if (int rc = need(2)) return rc;
         if (!fits_i32(d[0] * d[1])) return set_error(PHX_E_INVALID, "matmul_init exceeds i32 index");
@@ -223,11 +226,12 @@ int check_shape(phx_kernel k, const int64_t *d, int nd) {
     case PHX_FLASH_FP32:
     case PHX_FLASH_FP16:
         if (int rc = need(3)) return rc;
-        if (d[2] != PHX_FA_D || d[0] == 0 || d[1] == 0 || d[0] % PHX_FA_BR || d[1] % PHX_FA_BC)
-            return set_error(PHX_E_INVALID,
-                             "flash needs D==%d, Nq%%%d==0, Nk%%%d==0 (got Nq=%lld Nk=%lld D=%lld)",
-                             PHX_FA_D, PHX_FA_BR, PHX_FA_BC, (long long)d[0], (long long)d[1],
-                             (long long)d[2]);
+        if (d[2] != PHX_FA_D || d[0] == 0 || d[1] == 0)
+            return set_error(PHX_E_INVALID, "flash needs D==%d, Nq>0, Nk>0 (got Nq=%lld Nk=%lld D=%lld)",
+                             PHX_FA_D, (long long)d[0], (long long)d[1], (long long)d[2]);
+        if (d[0] * PHX_FA_D * 4 > INT32_MAX || d[1] * PHX_FA_D * 4 > INT32_MAX)
+            return set_error(PHX_E_INVALID, "flash head exceeds 2 GiB (Nq=%lld Nk=%lld)",
+                             (long long)d[0], (long long)d[1]);
         return PHX_OK;
     case PHX_FLASH_FP32_BH:
     case PHX_FLASH_FP16_BH:
@@ -255,7 +259,7 @@ int grid_for(phx_kernel k, const int64_t *d, int nd, uint32_t grid[3], uint32_t 
     }
     case PHX_GEMM_FP16TC_FP32ACC:
     case PHX_GEMM_FP16:
-        grid[0] = (uint32_t)((d[0] / PHX_H_BM) * (d[1] / PHX_H_BN));
+        grid[0] = (uint32_t)(((d[0] + PHX_H_BM - 1) / PHX_H_BM) * ((d[1] + PHX_H_BN - 1) / PHX_H_BN));
         break;
     case PHX_GEMM_FP32:
     case PHX_MATMUL:
@@ -269,13 +273,13 @@ int grid_for(phx_kernel k, const int64_t *d, int nd, uint32_t grid[3], uint32_t 
         break;
     }
     case PHX_FLASH_FP32:
-        grid[0] = (uint32_t)(d[0] / PHX_FA_BR);
+        grid[0] = (uint32_t)((d[0] + PHX_FA_BR - 1) / PHX_FA_BR);
         break;
     case PHX_FLASH_FP16:
         grid[0] = (uint32_t)((d[0] + PHX_FA16_BR - 1) / PHX_FA16_BR);
         break;
     case PHX_FLASH_FP32_BH:
-        grid[0] = (uint32_t)(d[1] / PHX_FA_BR);
+        grid[0] = (uint32_t)((d[1] + PHX_FA_BR - 1) / PHX_FA_BR);
         grid[1] = (uint32_t)d[0];
         break;
     case PHX_FLASH_FP16_BH:
@@ -544,6 +548,7 @@ static int launch_builtin(phx_kernel k, const int64_t *dims, int nd, ArgPack &pa
 }
 
 int phx_saxpy(phx_stream s, uint64_t x, uint64_t y, uint64_t out, int64_t n, float alpha) {
+    if (n > 0 && (!x || !y || !out)) return set_error(PHX_E_INVALID, "saxpy: null operand");
     int64_t d[1] = {n};
     ArgPack p(20);
     p.memref(x, d, 1, 32);
@@ -558,6 +563,8 @@ int phx_gemm(phx_stream s, phx_kernel k, uint64_t a, uint64_t b, uint64_t c, int
     if (k != PHX_GEMM_FP32 && k != PHX_GEMM_FP16TC_FP32ACC && k != PHX_GEMM_FP16 &&
         k != PHX_MATMUL)
         return set_error(PHX_E_INVALID, "kernel %d is not a gemm", (int)k);
+    if (!a || !b || !c) return set_error(PHX_E_INVALID, "gemm: null operand");
+    if ((a | b | c) & 15) return set_error(PHX_E_INVALID, "gemm operands must be 16-byte aligned");
     int bits = kSpecs[k].index_bits;
     int64_t d[3] = {M, N, K};
     int64_t sa[2] = {M, K}, sb[2] = {K, N}, sc[2] = {M, N};
@@ -571,6 +578,7 @@ int phx_gemm(phx_stream s, phx_kernel k, uint64_t a, uint64_t b, uint64_t c, int
 }
 
 int phx_matmul_init(phx_stream s, uint64_t c, int64_t M, int64_t N, float beta) {
+    if (!c) return set_error(PHX_E_INVALID, "matmul_init: null operand");
     int64_t d[2] = {M, N};
     ArgPack p(10);
     p.memref(c, d, 2, 32);
@@ -582,6 +590,8 @@ int phx_flash_attention(phx_stream s, phx_kernel k, uint64_t q, uint64_t kk, uin
                         uint64_t o, int64_t Nq, int64_t Nk, int64_t D, float scale) {
     if (k != PHX_FLASH_FP32 && k != PHX_FLASH_FP16)
         return set_error(PHX_E_INVALID, "kernel %d is not a single-head flash", (int)k);
+    if (!q || !kk || !v || !o) return set_error(PHX_E_INVALID, "flash: null operand");
+    if ((q | kk | v | o) & 15) return set_error(PHX_E_INVALID, "flash operands must be 16-byte aligned");
     int64_t d[3] = {Nq, Nk, D};
     int64_t sq[2] = {Nq, D}, sk[2] = {Nk, D};
     ArgPack p(32);
@@ -598,6 +608,8 @@ int phx_flash_attention_bh(phx_stream s, phx_kernel k, uint64_t q, uint64_t kk, 
                            float scale) {
     if (k != PHX_FLASH_FP32_BH && k != PHX_FLASH_FP16_BH)
         return set_error(PHX_E_INVALID, "kernel %d is not a batched flash", (int)k);
+    if (!q || !kk || !v || !o) return set_error(PHX_E_INVALID, "flash: null operand");
+    if ((q | kk | v | o) & 15) return set_error(PHX_E_INVALID, "flash operands must be 16-byte aligned");
     int64_t d[4] = {BH, Nq, Nk, D};
     int64_t sq[3] = {BH, Nq, D}, sk[3] = {BH, Nk, D};
     ArgPack p(44);

@@ -80,7 +80,35 @@ def test_grid_for_and_shape_checks():
     assert px.check_shape(px.FLASH_FP32, [4096, 4096, 128]) == px.PHX_E_INVALID
     assert px.check_shape(px.GEMM_FP32, [1 << 16, 1 << 16, 128]) == px.PHX_E_INVALID  # i32 idx
     assert px.check_shape(px.SAXPY_FP32, [1 << 31]) == px.PHX_E_INVALID
-    assert "f16 gemm needs" in px.lib().phx_last_error().decode() or True
+
+
+def test_ragged_shape_rules():
+    # The reference's autotuner accepts M, N multiples of its smallest tile
+    # (32) and K of its K tile (16 for f16, 4 for f32); these kernels accept
+    # every such shape and more: M any, N and K whole 16-byte chunks (K % 8
+    # for gemm_fp16tc), flash any Nq and Nk.
+    ok = px.check_shape
+    for M, N, K in [(96, 100, 64), (1, 4, 4), (257, 516, 1000), (32, 32, 16)]:
+        assert ok(px.GEMM_FP32, [M, N, K]) == 0, (M, N, K)
+        assert ok(px.MATMUL, [M, N, K]) == 0
+    assert ok(px.GEMM_FP16TC_FP32ACC, [96, 100, 64]) == 0
+    assert ok(px.GEMM_FP16TC_FP32ACC, [96, 100, 60]) == px.PHX_E_INVALID  # K % 8
+    assert ok(px.GEMM_FP16, [96, 104, 64]) == 0
+    assert ok(px.GEMM_FP16, [96, 100, 64]) == px.PHX_E_INVALID             # N % 8
+    assert ok(px.GEMM_FP32, [96, 102, 64]) == px.PHX_E_INVALID             # N % 4
+    assert "N%4==0" in px.lib().phx_last_error().decode()
+    assert ok(px.GEMM_FP32, [0, 4, 4]) == px.PHX_E_INVALID
+    g, _ = px.grid_for(px.GEMM_FP16, [300, 264, 40])    # 2 x 2 tiles of 256
+    assert g == (4, 1, 1)
+    g, _ = px.grid_for(px.GEMM_FP16TC_FP32ACC, [1, 4, 8])
+    assert g == (1, 1, 1)
+    for k in (px.FLASH_FP32, px.FLASH_FP16):
+        for Nq, Nk in [(1, 1), (100, 37), (300, 200)]:
+            assert ok(k, [Nq, Nk, 64]) == 0, (k, Nq, Nk)
+        assert ok(k, [0, 64, 64]) == px.PHX_E_INVALID
+        assert ok(k, [64, 0, 64]) == px.PHX_E_INVALID
+    assert px.grid_for(px.FLASH_FP32, [300, 37, 64])[0] == (3, 1, 1)   # 128-row workgroups
+    assert px.grid_for(px.FLASH_FP16_BH, [5, 300, 37, 64])[0] == (2, 5, 1)
 
 
 def test_kernel_abi_index_widths():

@@ -3,6 +3,7 @@
 phx_compute builds the exploded-memref argument list exactly as
 Engine::launch does (phobos-pod/src/engine.rs:582-647), with scalars placed by
 ScalarArg.pos; the kernels accept the reference-derived grid and cta."""
+import ctypes
 import os
 
 import numpy as np
@@ -80,13 +81,32 @@ def test_matmul_init_ragged_and_exact(px_gpu, stream):
         assert np.array_equal(got.view(np.uint32), oracle.matmul_init(1.5, C).view(np.uint32))
 
 
-def test_gemm_rejects_bad_shapes(px_gpu, stream):
+def test_launches_reject_bad_shapes_and_null_operands(px_gpu, stream):
+    # Shapes outside the kernels' contract and null operands are refused on
+    # the host before anything is launched.  Real buffers throughout, so a
+    # check that let one through could not reach a null address.
     px = px_gpu
+    buf = px.DeviceBuffer(1 << 20)
+    p = buf.ptr
     with pytest.raises(px.PhxError) as e:
-        px.launch_gemm(stream, px.GEMM_FP16, 0, 0, 0, 4096, 100, 4096, 1.0, 0.0)
+        px.launch_gemm(stream, px.GEMM_FP16, p, p, p, 64, 100, 64, 1.0, 0.0)   # N % 8
     assert e.value.code == px.PHX_E_INVALID
     with pytest.raises(px.PhxError):
-        px.launch_flash(stream, px.FLASH_FP16, 0, 0, 0, 0, 100, 4096, 64, 0.125)
+        px.launch_gemm(stream, px.GEMM_FP32, p, p, p, 64, 64, 30, 1.0, 0.0)    # K % 4
+    with pytest.raises(px.PhxError):
+        px.launch_flash(stream, px.FLASH_FP16, p, p, p, p, 16, 16, 128, 0.125)  # D != 64
+    with pytest.raises(px.PhxError):
+        px.launch_flash(stream, px.FLASH_FP32, p, p, p, p, 0, 16, 64, 0.125)   # Nq = 0
+    with pytest.raises(px.PhxError):
+        px.launch_gemm(stream, px.GEMM_FP32, p + 4, p, p, 64, 64, 64, 1.0, 0.0)  # misaligned
+    for call in (lambda: px.lib().phx_gemm(stream.handle, px.GEMM_FP32, 0, p, p, 64, 64, 64,
+                                           ctypes.c_float(1.0), ctypes.c_float(0.0)),
+                 lambda: px.lib().phx_flash_attention(stream.handle, px.FLASH_FP16, p, p, 0, p,
+                                                      16, 16, 64, ctypes.c_float(0.125)),
+                 lambda: px.lib().phx_saxpy(stream.handle, p, 0, p, 16, ctypes.c_float(1.0))):
+        assert call() == px.PHX_E_INVALID
+        assert "null operand" in px.lib().phx_last_error().decode()
+    stream.synchronize()
 
 
 @pytest.mark.parametrize("kernel,grid", [("GEMM_FP16", 2), ("GEMM_FP16TC_FP32ACC", 4),

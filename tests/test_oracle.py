@@ -189,6 +189,25 @@ def test_flash_against_closed_form_and_invariants():
     assert np.allclose(o32, got, rtol=1e-4, atol=1e-5)
 
 
+def test_flash_any_scale_sign_and_ragged_keys():
+    # negative and zero scales and key counts that are not block multiples:
+    # the replay is per key, so it must match the closed form for any of them
+    rng = np.random.default_rng(10)
+    D = 16
+    for Nq, Nk, scale in [(7, 37, -0.5), (3, 1, 0.25), (5, 65, 0.0), (4, 130, -3.0)]:
+        q = rng.standard_normal((Nq, D)).astype(np.float32)
+        k = rng.standard_normal((Nk, D)).astype(np.float32)
+        v = rng.standard_normal((Nk, D)).astype(np.float32)
+        got = oracle.flash_rows(np.arange(Nq), q, k, v, scale)
+        assert np.allclose(got, _softmax_attention(q, k, v, scale), rtol=1e-10, atol=1e-12), scale
+    # scale 0: every key weighs the same
+    got = oracle.flash_rows(np.arange(Nq), q, k, v, 0.0)
+    assert np.allclose(got, np.broadcast_to(v.astype(np.float64).mean(0), got.shape), atol=1e-12)
+    # a sign error in the scale would pick the opposite softmax
+    assert not np.allclose(oracle.flash_rows(np.arange(Nq), q, k, v, -3.0),
+                           _softmax_attention(q, k, v, 3.0), atol=1e-3)
+
+
 # ------------------------------------------------------- cluster chain
 def test_cluster_chain_matches_direct_evaluation():
     rng = np.random.default_rng(4)
