@@ -96,6 +96,10 @@ __device__ __forceinline__ float xor32_add(float x) {
     return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
 }
 
+typedef __attribute__((address_space(3))) void *phx_lds_vp;
+// s_waitcnt fields: vmcnt [3:0]+[15:14], expcnt [6:4], lgkmcnt [11:8]
+#define PHX_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14))
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t phx_rsrc(const void *p, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes,
                                              0x00020000);
@@ -187,9 +191,7 @@ __device__ __forceinline__ float softmax_c2(float scale) {
 
 typedef __fp16 phx_fp16x4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
 typedef __attribute__((address_space(3))) phx_fp16x4 *phx_lds_h4p;
-typedef __attribute__((address_space(3))) void *phx_lds_vp;
 
-#define PHX_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14))
 #define PHX_WAIT_VM_LGKM0(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (((n) >> 4) << 14))
 
 #define SGB(mask, n) __builtin_amdgcn_sched_group_barrier(mask, n, 0)
@@ -524,71 +526,59 @@ __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp
 __device__ __forceinline__ uint32_t vt_off(uint32_t row, uint32_t chunk) {
     return row * ROW_BYTES + ((chunk ^ ((row ^ (row >> 2)) & 15)) << 4);
 }
-// K rows / V^T rows are 64 floats (256 B, 16 chunks).  Waves 0-1 stage V^T
-// via 4x4 register transposes, waves 2-3 stage K; 8 x 16-byte loads each.
-// In a partial last block (rows past Nk) every row index is clamped to Nk-1:
-// those rows hold finite copies of the last key, whose scores the block's
-// mask sets to -inf, so they add nothing.  (Global loads: buffer loads with a
-// bounded resource measured 3.5% slower here.)
+// K rows / V^T rows are 64 floats (256 B, 16 chunks).  K is copied global ->
+// LDS directly (buffer_load ... lds: a 64-lane copy fills 4 rows; lane l lands
+// at row r = l/16 (+4c), physical chunk l%16 and fetches the logical chunk
+// (l%16) ^ (r & 15) stored there), 4 copies per wave, through a resource that
+// ends at key Nk (rows past it read zero).  V^T is staged by all 256 threads,
+// one 4x4 register transpose each: keys 4kq .. +3, d = 4dq .. +3.  In a
+// partial last block V rows past Nk repeat row Nk-1 (finite; those keys'
+// scores are masked to -inf, so their p is 0).
 struct Stage {
-    phx_f4 r[8];
+    phx_f4 r[4];
 };
 
+__device__ __forceinline__ void dma_k(char *Ks, const T *Kp, int64_t ldk, uint32_t Nk,
+                                      uint32_t blk, const uint32_t (&vk)[4], uint32_t wave) {
+    const __amdgpu_buffer_rsrc_t rk = kv_rsrc(Kp, ldk, Nk, blk);
+#pragma unroll
+    for (int c = 0; c < 4; ++c)  // rows 16 wave + 4c .. +3
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rk, (phx_lds_vp)(Ks + (16 * wave + 4 * c) * ROW_BYTES), 16, vk[c],
+            (int)((uint32_t)((16 * wave + 4 * c) * ldk) * 4), 0, 0);
+}
+
 template <bool CLAMP>
-__device__ __forceinline__ void load_stage_rows(Stage &st, const T *Kp, const T *Vp, int64_t ldk,
-                                                int64_t ldv, uint32_t Nk, uint32_t key0,
-                                                uint32_t tid) {
-    auto row = [&](uint32_t r) { return CLAMP ? (r < Nk ? r : Nk - 1) : r; };
-    if (tid < 128) {
-        // two 4x4 blocks: keys 4kq..4kq+3 (kq = v/16 and kq+8), d = 4*(v%16)..
-        const uint32_t v = tid, dq = v & 15, kq = v >> 4;
+__device__ __forceinline__ void load_v_rows(Stage &st, const T *Vp, int64_t ldv, uint32_t Nk,
+                                            uint32_t key0, uint32_t tid) {
+    const uint32_t dq = tid & 15, kq = tid >> 4;
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                st.r[4 * h + i] =
-                    *(const phx_f4 *)(Vp + (int64_t)row(key0 + 4 * (kq + 8 * h) + i) * ldv + 4 * dq);
-    } else {
-        const uint32_t u = tid - 128;  // 64 rows x 16 chunks = 1024 = 128 x 8
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-            st.r[i] = *(const phx_f4 *)(Kp + (int64_t)row(key0 + i * 8 + (u >> 4)) * ldk + 4 * (u & 15));
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t r = key0 + 4 * kq + i;
+        st.r[i] = *(const phx_f4 *)(Vp + (int64_t)(CLAMP ? (r < Nk ? r : Nk - 1) : r) * ldv + 4 * dq);
     }
 }
 
-__device__ __forceinline__ void load_stage(Stage &st, const T *Kp, const T *Vp, int64_t ldk,
-                                           int64_t ldv, uint32_t Nk, uint32_t blk, uint32_t tid) {
+__device__ __forceinline__ void load_v(Stage &st, const T *Vp, int64_t ldv, uint32_t Nk,
+                                       uint32_t blk, uint32_t tid) {
     const uint32_t key0 = blk * BC;
     if (key0 + BC <= Nk)  // wave-uniform
-        load_stage_rows<false>(st, Kp, Vp, ldk, ldv, Nk, key0, tid);
+        load_v_rows<false>(st, Vp, ldv, Nk, key0, tid);
     else
-        load_stage_rows<true>(st, Kp, Vp, ldk, ldv, Nk, key0, tid);
+        load_v_rows<true>(st, Vp, ldv, Nk, key0, tid);
 }
 
-__device__ __forceinline__ void store_stage(const Stage &st, char *Ks, char *Vt, uint32_t tid) {
-    if (tid < 128) {
-        const uint32_t v = tid, dq = v & 15, kq = v >> 4;
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const phx_f4 *b = &st.r[4 * h];
-            const uint32_t chunk = kq + 8 * h;  // keys 4*chunk .. +3
-            phx_f4 c0 = {b[0].x, b[1].x, b[2].x, b[3].x};
-            phx_f4 c1 = {b[0].y, b[1].y, b[2].y, b[3].y};
-            phx_f4 c2 = {b[0].z, b[1].z, b[2].z, b[3].z};
-            phx_f4 c3 = {b[0].w, b[1].w, b[2].w, b[3].w};
-            *(phx_f4 *)(Vt + vt_off(4 * dq + 0, chunk)) = c0;
-            *(phx_f4 *)(Vt + vt_off(4 * dq + 1, chunk)) = c1;
-            *(phx_f4 *)(Vt + vt_off(4 * dq + 2, chunk)) = c2;
-            *(phx_f4 *)(Vt + vt_off(4 * dq + 3, chunk)) = c3;
-        }
-    } else {
-        const uint32_t u = tid - 128;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t row = i * 8 + (u >> 4), ch = u & 15;
-            *(phx_f4 *)(Ks + lds_off(row, ch)) = st.r[i];
-        }
-    }
+__device__ __forceinline__ void store_v(const Stage &st, char *Vt, uint32_t tid) {
+    const uint32_t dq = tid & 15, kq = tid >> 4;  // keys 4*kq .. +3 = V^T chunk kq
+    const phx_f4 *b = st.r;
+    const phx_f4 c0 = {b[0].x, b[1].x, b[2].x, b[3].x};
+    const phx_f4 c1 = {b[0].y, b[1].y, b[2].y, b[3].y};
+    const phx_f4 c2 = {b[0].z, b[1].z, b[2].z, b[3].z};
+    const phx_f4 c3 = {b[0].w, b[1].w, b[2].w, b[3].w};
+    *(phx_f4 *)(Vt + vt_off(4 * dq + 0, kq)) = c0;
+    *(phx_f4 *)(Vt + vt_off(4 * dq + 1, kq)) = c1;
+    *(phx_f4 *)(Vt + vt_off(4 * dq + 2, kq)) = c2;
+    *(phx_f4 *)(Vt + vt_off(4 * dq + 3, kq)) = c3;
 }
 
 #define RESCALE_SLACK 8.0f
@@ -619,14 +609,27 @@ __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp
     float l = 0.0f;
 
     const uint32_t nkb = (Nk + BC - 1) / BC;
+    // K copy sources of this lane: row lane/16 of copy c's 4-row group (rows
+    // 16 wave + 4c + lane/16, so row & 15 = 4c + lane/16), logical chunk
+    // (lane%16) ^ (row & 15)
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(wave);
+    uint32_t vk[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+        vk[c] = (uint32_t)(((lane >> 4) * ldk + 4 * ((lane & 15) ^ (4 * c + (lane >> 4)))) * 4);
     Stage st;
-    load_stage(st, Kp, Vp, ldk, ldv, Nk, 0, tid);
-    store_stage(st, lds[0][0], lds[0][1], tid);
+    dma_k(lds[0][0], Kp, ldk, Nk, 0, vk, wv);
+    load_v(st, Vp, ldv, Nk, 0, tid);
+    store_v(st, lds[0][1], tid);
+    PHX_WAIT_VMCNT(0);
     __syncthreads();
 
     for (uint32_t kb = 0; kb < nkb; ++kb) {
         const uint32_t cur = kb & 1;
-        if (kb + 1 < nkb) load_stage(st, Kp, Vp, ldk, ldv, Nk, kb + 1, tid);
+        if (kb + 1 < nkb) {
+            dma_k(lds[cur ^ 1][0], Kp, ldk, Nk, kb + 1, vk, wv);
+            load_v(st, Vp, ldv, Nk, kb + 1, tid);
+        }
         const char *Ks = lds[cur][0];
         const char *Vt = lds[cur][1];
 
@@ -687,7 +690,8 @@ __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp
                                                                        acc[dt], 0, 0, 0);
                 }
 
-        if (kb + 1 < nkb) store_stage(st, lds[cur ^ 1][0], lds[cur ^ 1][1], tid);
+        if (kb + 1 < nkb) store_v(st, lds[cur ^ 1][1], tid);
+        PHX_WAIT_VMCNT(0);  // this wave's K copies of block kb+1 landed
         __syncthreads();
     }
 
