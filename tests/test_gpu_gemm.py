@@ -177,3 +177,36 @@ def test_gemm_fp32_baseline_config_sampled(px_gpu, stream):
     g = got[r.astype(int), c.astype(int)]
     rel = np.abs(g - want) / np.maximum(np.abs(want), np.finfo(np.float64).tiny)
     assert rel.max() < 1e-4, rel.max()
+
+
+def test_gemm_fp16_operand_past_4gib(px_gpu, stream):
+    # A of 2^21 x 1024 f16 (4 GiB): tiles past the 4 GiB mark address A
+    # through 64-bit tile bases.  A's rows repeat with period 3001 (built by
+    # device copies), which does not divide the 2^21 rows, so a row fetched
+    # through a wrapped 32-bit offset would come from the wrong phase.
+    px = px_gpu
+    M, N, K, P = 1 << 21, 256, 1024, 3001
+    Ap = oracle.f16_round(oracle.normal_f32(61, P * K, 1 / 32)).reshape(P, K)
+    B = oracle.f16_round(oracle.normal_f32(62, K * N, 1 / 32)).reshape(K, N)
+    dA = px.DeviceBuffer(M * K * 2)
+    blk = oracle.f16_bits(Ap)
+    dA.upload(blk)
+    rows = P
+    while rows < M:  # double the filled prefix
+        m = min(rows, M - rows)
+        assert px.lib().phx_memcpy_d2d(dA.ptr + rows * K * 2, dA.ptr, m * K * 2) == 0
+        rows += m
+    dB = px.DeviceBuffer.from_array(oracle.f16_bits(B))
+    dC = px.DeviceBuffer(M * N * 2)
+    print(f"gemm_fp16 M={M} N={N} K={K}", flush=True)
+    px.launch_gemm(stream, px.GEMM_FP16, dA, dB, dC, M, N, K, 1.0, 0.0)
+    stream.synchronize()
+    want = oracle.gemm_full(Ap, B, None, 1.0, 0.0, round16=True)   # one period
+    rms = np.sqrt(np.mean(want ** 2))
+    out = np.empty(N, np.uint16)
+    for r in [0, 1, P - 1, P, (1 << 20) + 7, (1 << 21) - 4097, M - 2, M - 1]:
+        assert px.lib().phx_memcpy_d2h(out.ctypes.data, dC.ptr + r * N * 2, N * 2) == 0
+        got = oracle.f16_to_f32(out)
+        assert np.abs(got - want[r % P]).max() / rms < 2e-2, r
+    for b in (dA, dB, dC):
+        b.free()

@@ -62,3 +62,30 @@ def test_saxpy_unaligned_offset_path(px_gpu, stream):
     want = oracle.saxpy(np.float32(-1.25), x[1:], y[1:])
     assert got[0] == y[0]
     assert np.array_equal(got[1:].view(np.uint32), want.view(np.uint32))
+
+
+def test_saxpy_max_i32_extent(px_gpu, stream):
+    # n = 2^31 - 1, the largest extent the i32 descriptor holds (three 8 GiB
+    # vectors, which 288 GB of HBM takes easily): the chunks past 4 GiB get
+    # their own buffer resources and the last 3 elements are the ragged tail.
+    # x and y are byte-pattern fills, so every output is the same f32 value.
+    px = px_gpu
+    n = (1 << 31) - 1
+    dx, dy, do = (px.DeviceBuffer(n * 4) for _ in range(3))
+    for b, byte in ((dx, 0x3F), (dy, 0x40), (do, 0x00)):
+        assert px.lib().phx_memset_async(b.ptr, byte, b.nbytes, stream.handle) == 0
+    print(f"saxpy n={n}", flush=True)
+    px.launch_saxpy(stream, dx, dy, do, n, 2.5)
+    stream.synchronize()
+    x = np.frombuffer(bytes([0x3F] * 4), np.float32)
+    y = np.frombuffer(bytes([0x40] * 4), np.float32)
+    want = oracle.saxpy(np.float32(2.5), x, y).view(np.uint32)[0]
+    chunk = 1 << 26  # elements per download (256 MiB)
+    buf = np.empty(chunk, np.uint32)
+    for start in range(0, n, chunk):
+        m = min(chunk, n - start)
+        assert px.lib().phx_memcpy_d2h(buf.ctypes.data, do.ptr + 4 * start, 4 * m) == 0
+        bad = np.flatnonzero(buf[:m] != want)
+        assert bad.size == 0, (start + bad[:4], buf[bad[:4]], want)
+    for b in (dx, dy, do):
+        b.free()
