@@ -129,3 +129,22 @@ def test_calls_before_init_fail_loudly():
         pytest.skip("already initialised in this process")
     rc = px.lib().phx_builtin_function(ctypes.byref(f), px.GEMM_FP16)
     assert rc == px.PHX_E_NOT_INIT
+
+
+def test_rust_ffi_stub_matches_header():
+    # INTEGRATION.md's phobos-hip-sys block (the binding the reference's
+    # Rust side would add) declares every function of include/phobos_hip.h
+    # with the same number of parameters.
+    import re
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    h = re.sub(r"/\*.*?\*/", "", open(os.path.join(root, "include", "phobos_hip.h")).read(), flags=re.S)
+    decls = {n: 0 if p.strip() in ("", "void") else p.count(",") + 1
+             for n, p in re.findall(r"^(?:int|const char \*|size_t|void)\s*(phx_\w+)\s*\(([^;]*?)\)\s*;",
+                                    h, flags=re.M)}
+    md = open(os.path.join(root, "INTEGRATION.md")).read()
+    block = md[md.index('#[link(name = "phobos_hip")]'):]
+    block = block[:block.index("}\n```")]
+    rs = {n: 0 if not p.strip() else p.count(",") + 1
+          for n, p in re.findall(r"pub fn (phx_\w+)\(([^)]*)\)", block)}
+    assert len(decls) >= 60
+    assert rs == decls
