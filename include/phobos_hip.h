@@ -123,6 +123,19 @@ int phx_launch(phx_function f, const uint32_t grid[3], const uint32_t block[3],
  * 1220-1223; phobos-sched/src/lib.rs:380-429). */
 int phx_grid_for(phx_kernel k, const int64_t *dims, int ndims, uint32_t grid[3],
                  uint32_t block[3]);
+/* Kernel id of a built-in by the reference's names: the .ph file stem
+ * ("saxpy_fp32", "gemm_fp32", "gemm_fp16tc_fp32acc", "gemm_fp16",
+ * "flash_attention_fp32", "flash_attention_fp16", "matmul_cluster_fp32") and
+ * the kernel's entry name ("saxpy", "gemm", "flash_attention",
+ * "flash_attention_bh", "matmul", "matmul_init").  The stem is needed: three
+ * .ph files export "gemm" (phobos-bench/src/main.rs:512, 761, 985;
+ * clustergen.rs:1285, 1353).  PHX_E_INVALID for an unknown pair. */
+int phx_kernel_by_name(phx_kernel *k, const char *ph_file, const char *entry);
+/* phx_launch of the built-in phx_kernel_by_name names, with the caller's
+ * void** argument list (the launch! macro's, main.rs:308-323).  block NULL
+ * means the kernel's own workgroup size (phx_kernel_abi). */
+int phx_launch_by_name(const char *ph_file, const char *entry, const uint32_t grid[3],
+                       const uint32_t block[3], phx_stream s, void **args);
 /* Validates that a built-in kernel accepts these dims (divisibility etc). */
 int phx_check_shape(phx_kernel k, const int64_t *dims, int ndims);
 

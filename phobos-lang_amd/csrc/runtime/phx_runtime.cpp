@@ -487,6 +487,28 @@ int phx_builtin_function(phx_function *f, phx_kernel k) {
 int phx_kernel_abi(phx_kernel k, int *index_bits, uint32_t block[3]) {
     return kernel_abi(k, index_bits, block);
 }
+int phx_kernel_by_name(phx_kernel *k, const char *ph_file, const char *entry) {
+    if (!k || !ph_file || !entry) return set_error(PHX_E_INVALID, "kernel_by_name: null argument");
+    const size_t n = strlen(ph_file);
+    for (int i = 0; i < PHX_NUM_KERNELS; ++i) {
+        const char *f = kSpecs[i].file;  // "<stem>.hsaco"
+        if (strncmp(f, ph_file, n) == 0 && strcmp(f + n, ".hsaco") == 0 &&
+            strcmp(kSpecs[i].entry, entry) == 0) {
+            *k = (phx_kernel)i;
+            return PHX_OK;
+        }
+    }
+    return set_error(PHX_E_INVALID, "no built-in kernel %s:%s", ph_file, entry);
+}
+int phx_launch_by_name(const char *ph_file, const char *entry, const uint32_t grid[3],
+                       const uint32_t block[3], phx_stream s, void **args) {
+    phx_kernel k;
+    if (int rc = phx_kernel_by_name(&k, ph_file, entry)) return rc;
+    phx_function f;
+    if (int rc = phx_builtin_function(&f, k)) return rc;
+    uint32_t own[3] = {kSpecs[k].block, 1, 1};
+    return phx_launch(f, grid, block ? block : own, 0, s, args);
+}
 
 // ------------------------------------------------------------------ launch
 int phx_launch(phx_function f, const uint32_t grid[3], const uint32_t block[3],

@@ -107,6 +107,9 @@ def lib():
     L.phx_host_free.argtypes = [_vp]
     L.phx_memcpy_h2d.argtypes = [_u64, _vp, _sz]
     L.phx_memcpy_d2h.argtypes = [_vp, _u64, _sz]
+    L.phx_kernel_by_name.argtypes = [ctypes.POINTER(ctypes.c_int), ctypes.c_char_p, ctypes.c_char_p]
+    L.phx_launch_by_name.argtypes = [ctypes.c_char_p, ctypes.c_char_p, _vp, _vp, _vp,
+                                     ctypes.POINTER(ctypes.c_void_p)]
     L.phx_memcpy_d2d.argtypes = [_u64, _u64, _sz]
     L.phx_memcpy_h2d_async.argtypes = [_u64, _vp, _sz, _vp]
     L.phx_memcpy_d2h_async.argtypes = [_vp, _u64, _sz, _vp]
@@ -348,6 +351,13 @@ def grid_for(kernel, dims):
     g, b = _u32a3(), _u32a3()
     check(lib().phx_grid_for(kernel, d, len(dims), g, b))
     return tuple(g), tuple(b)
+
+
+def kernel_by_name(ph_file, entry):
+    """Built-in kernel id for the reference's .ph file stem and entry name."""
+    k = ctypes.c_int()
+    check(lib().phx_kernel_by_name(ctypes.byref(k), ph_file.encode(), entry.encode()))
+    return k.value
 
 
 def check_shape(kernel, dims):

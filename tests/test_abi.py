@@ -111,6 +111,24 @@ def test_ragged_shape_rules():
     assert px.grid_for(px.FLASH_FP16_BH, [5, 300, 37, 64])[0] == (2, 5, 1)
 
 
+def test_kernel_by_reference_names():
+    # (.ph file stem, entry) -> kernel id; three files export "gemm"
+    want = {("saxpy_fp32", "saxpy"): px.SAXPY_FP32, ("gemm_fp32", "gemm"): px.GEMM_FP32,
+            ("gemm_fp16tc_fp32acc", "gemm"): px.GEMM_FP16TC_FP32ACC,
+            ("gemm_fp16", "gemm"): px.GEMM_FP16,
+            ("flash_attention_fp32", "flash_attention"): px.FLASH_FP32,
+            ("flash_attention_fp16", "flash_attention"): px.FLASH_FP16,
+            ("flash_attention_fp32", "flash_attention_bh"): px.FLASH_FP32_BH,
+            ("flash_attention_fp16", "flash_attention_bh"): px.FLASH_FP16_BH,
+            ("matmul_cluster_fp32", "matmul"): px.MATMUL,
+            ("matmul_cluster_fp32", "matmul_init"): px.MATMUL_INIT}
+    for (f, e), k in want.items():
+        assert px.kernel_by_name(f, e) == k, (f, e)
+    for f, e in [("gemm", "gemm"), ("gemm_fp16tc", "gemm"), ("saxpy_fp32", "gemm")]:
+        with pytest.raises(px.PhxError):
+            px.kernel_by_name(f, e)
+
+
 def test_kernel_abi_index_widths():
     # requires_wide_index: @tensorcore kernels use i64 descriptors (lib.rs:47-49)
     assert px.kernel_abi(px.SAXPY_FP32)[0] == 32

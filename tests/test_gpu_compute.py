@@ -136,3 +136,29 @@ def test_f16_gemms_any_grid(px_gpu, stream, kernel, grid):
     stream.synchronize()
     dt = np.uint16 if f16 else np.uint32
     assert np.array_equal(dC.download(dt, M * N), dR.download(dt, M * N))
+
+
+def test_launch_by_reference_names_with_void_args(px_gpu, stream):
+    # phx_launch_by_name takes the reference's launch! argument list: one
+    # pointer per kernel parameter, each memref exploded as (alloc, aligned,
+    # offset, size, stride) at the kernel's index width (i32 for saxpy,
+    # main.rs:1230-1235), then the f32 scalar.
+    px = px_gpu
+    n = 10_007
+    x, y = oracle.lcg_f32(5, n), oracle.lcg_f32(6, n)
+    dx, dy = px.DeviceBuffer.from_array(x), px.DeviceBuffer.from_array(y)
+    do = px.DeviceBuffer(n * 4)
+    vals = []
+    for b in (dx, dy, do):
+        vals += [ctypes.c_void_p(b.ptr), ctypes.c_void_p(b.ptr), ctypes.c_int32(0),
+                 ctypes.c_int32(n), ctypes.c_int32(1)]
+    vals.append(ctypes.c_float(2.5))
+    args = (ctypes.c_void_p * len(vals))(*[ctypes.cast(ctypes.pointer(v), ctypes.c_void_p) for v in vals])
+    grid = (ctypes.c_uint32 * 3)(*px.grid_for(px.SAXPY_FP32, [n])[0])
+    assert px.lib().phx_launch_by_name(b"saxpy_fp32", b"saxpy", grid, None, stream.handle, args) == 0
+    stream.synchronize()
+    want = oracle.saxpy(np.float32(2.5), x, y)
+    assert np.array_equal(do.download(np.float32, n).view(np.uint32), want.view(np.uint32))
+    # unknown names are refused before any launch
+    assert px.lib().phx_launch_by_name(b"gemm_fp64", b"gemm", grid, None, stream.handle, args) \
+        == px.PHX_E_INVALID
