@@ -81,7 +81,26 @@ def parse():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 3 device-to-device copies of 256 MiB (the plain copy the "
                          "FETCH_SIZE/WRITE_SIZE counters are scaled by) and exit")
-    return ap.parse_args()
+    ap.add_argument("--bench", default=None, metavar="NAME",
+                    help="run only one benchmark, as phobos-bench --bench NAME: one of "
+                         + ", ".join(BENCHES))
+    ap.add_argument("--autotune", default=None, metavar="SPEC",
+                    help="phobos-bench's tile pins; refused here: these kernels have one tiling each")
+    args = ap.parse_args()
+    if args.bench is not None:
+        # phobos-bench/src/main.rs:62-67, 109-115: one name from the list
+        if args.bench not in BENCHES:
+            ap.error(f"unknown --bench '{args.bench}'; available: {', '.join(BENCHES)}")
+        args.kernels = args.bench
+    if args.autotune is not None:
+        ap.error("--autotune pins the reference's TILE_M/TILE_N/TILE_K/BR/BC search; the MI355X "
+                 "kernels have one tiling each (GEMM 256x256, K step 32; flash 128 or 256 "
+                 "queries x 64 keys) and no search to pin")
+    return args
+
+
+# phobos-bench's benchmark names (phobos-bench/src/main.rs:26-33)
+BENCHES = ["saxpy_fp32", "gemm_fp32", "gemm_fp16tc_fp32acc", "gemm_fp16", "flash_fp32", "flash_fp16"]
 
 
 class Kernel:

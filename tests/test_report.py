@@ -49,3 +49,19 @@ def test_write_read_and_plot(tmp_path):
     subprocess.run([sys.executable, os.path.join(ROOT, "phobos-lang_amd", "plot.py"), str(path),
                     "-o", str(png)], check=True, capture_output=True, timeout=120)
     assert png.stat().st_size > 1000
+
+
+def test_bench_cli_mirrors_phobos_bench_flags():
+    # --bench NAME takes phobos-bench's names (main.rs:26-33, 62-67) and
+    # rejects others; --autotune pins have no search to pin here.
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    run = lambda *a: subprocess.run([sys.executable, os.path.join(root, "bench.py"), *a],
+                                    capture_output=True, text=True, timeout=120)
+    r = run("--bench", "gemm_fp8")
+    assert r.returncode == 2 and "available: saxpy_fp32, gemm_fp32" in r.stderr
+    r = run("--bench", "gemm_fp16", "--autotune", "TILE_M=256")
+    assert r.returncode == 2 and "no search to pin" in r.stderr
+    r = run("--help")
+    assert r.returncode == 0 and "--bench NAME" in r.stdout and "--csv" in r.stdout
