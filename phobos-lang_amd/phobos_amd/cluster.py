@@ -40,12 +40,15 @@ def tile_id(tensor, version, coord):
     return (tensor << 52) | (version << 36) | coord
 
 
-def lower_matmul(M, N, K, TM, TN, TK, alpha, beta, c_rmw=True, version=0):
+def lower_matmul(M, N, K, TM, TN, TK, alpha, beta, c_rmw=True, version=0, owns=None):
     """Instruction list (list of dicts) of the single-node plan.
 
     c_rmw=True is the alpha/beta GEMM (C read-modify-write, init leaf
     C = beta*C); c_rmw=False is a plain `C = acc` kernel (C write-only, no
-    LOAD of C, zero-init leaf), the form the planner's own tests pin."""
+    LOAD of C, zero-init leaf), the form the planner's own tests pin.
+    owns(pm, pn) -> bool keeps only the C supertiles a node owns (the
+    planner's owner-computes split, phobos-sched/src/lib.rs:217, 238); the
+    A and B supertiles they read are loaded by that node's segment."""
     assert M % TM == 0 and N % TN == 0 and K % TK == 0
     gm, gn, gk = M // TM, N // TN, K // TK
     super_shape = {A: (TM, TK), B: (TK, TN), C: (TM, TN)}
@@ -61,6 +64,8 @@ def lower_matmul(M, N, K, TM, TN, TK, alpha, beta, c_rmw=True, version=0):
     computes = []
     for pm in range(gm):
         for pn in range(gn):
+            if owns is not None and not owns(pm, pn):
+                continue
             scal = [(1, beta)] if c_rmw else []
             computes.append((INIT_LEAF, [(C, (pm, pn), "rmw" if c_rmw else "w")], scal))
             for k in range(gk):

@@ -191,3 +191,91 @@ def test_loopback_add_from_a_caller_code_object(px_gpu, tmp_path):
     assert np.array_equal(got.view(np.uint32), (x + y).view(np.uint32))
     pod.close()
     px.module_unload(mod)
+
+
+def _job_files(workdir, M, N, K):
+    paths = {t: os.path.join(workdir, f"{n}.tensor") for t, n in ((cl.A, "a"), (cl.B, "b"), (cl.C, "c"))}
+    shapes = {cl.A: (M, K), cl.B: (K, N), cl.C: (M, N)}
+    for t, seed in ((cl.A, 1), (cl.B, 2), (cl.C, 3)):
+        cl.init_tensor(paths[t], shapes[t], "random", seed)
+    return paths, shapes
+
+
+def _pod_for(paths, shapes, arena_bytes):
+    pod = cl.Pod(arena_bytes, 2)
+    for t in (cl.A, cl.B, cl.C):
+        pod.set_tensor(t, "file://" + paths[t], shapes[t])
+    pod.set_kernel(cl.STEP_LEAF, cl.MATMUL)
+    pod.set_kernel(cl.INIT_LEAF, cl.MATMUL_INIT)
+    return pod
+
+
+def _check_c(paths, M, N, K):
+    A = oracle.lcg_f32(1, M * K).reshape(M, K)
+    B = oracle.lcg_f32(2, K * N).reshape(K, N)
+    C = oracle.lcg_f32(3, M * N).reshape(M, N)
+    got = np.fromfile(paths[cl.C], np.float32).reshape(M, N)
+    want = oracle.gemm_full(A, B, C, 0.125, 1.5)
+    rel = np.abs(got - want) / np.abs(want)
+    assert rel.max() < 1e-4, rel.max()
+
+
+def test_several_pods_own_c_supertiles(px_gpu, tmp_path):
+    # cluster_correctness.rs:432-482 runs N in-process nodes on one GPU; here
+    # three pods, each owning the C supertiles (pm*gn + pn) % 3 == rank (the
+    # planner's block-cyclic owner-computes), run concurrently and write
+    # disjoint regions of the same C file.
+    import threading
+    M = N = K = 768
+    TM, TN, TK = 256, 256, 256
+    paths, shapes = _job_files(str(tmp_path), M, N, K)
+    gn = N // TN
+    errors, stats = [], [None] * 3
+
+    def node(rank):
+        try:
+            ins = cl.lower_matmul(M, N, K, TM, TN, TK, 0.125, 1.5,
+                                  owns=lambda pm, pn: (pm * gn + pn) % 3 == rank)
+            pod = _pod_for(paths, shapes, 64 << 20)
+            try:
+                stats[rank] = (pod.run(cl.segment_text(ins)), cl.count_ops(ins))
+            finally:
+                pod.close()
+        except Exception as e:  # reported below
+            errors.append((rank, e))
+
+    threads = [threading.Thread(target=node, args=(r,)) for r in range(3)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+    assert sum(st["compute"] for st, _ in stats) == (M // TM) * (N // TN) * (1 + K // TK)
+    for st, c in stats:
+        assert st["store"] == c["STORE"] == 3 and st["compute"] == c["COMPUTE"]
+    _check_c(paths, M, N, K)
+
+
+def test_job_split_into_segments_under_a_small_arena(px_gpu, tmp_path):
+    # budgeted.rs:53-137: a job larger than the pod's memory budget runs as
+    # more than one segment.  The arena holds one C row of supertiles with
+    # its A panel and all of B (24 of the job's 48 supertiles), so the 4 x 4
+    # supertile job runs as 4 segments, one per C supertile row, in turn,
+    # each reusing the memory the previous one freed.
+    M = N = K = 1024
+    TM, TN, TK = 256, 256, 256
+    paths, shapes = _job_files(str(tmp_path), M, N, K)
+    st_bytes = 4 * TM * TK
+    arena = st_bytes * (4 + 16 + 4) + (1 << 20)   # A row panel + all of B + a C row
+    full = 4 * (M * K + K * N + M * N)
+    assert arena < full
+    pod = _pod_for(paths, shapes, arena)
+    try:
+        total = 0
+        for row in range(M // TM):
+            ins = cl.lower_matmul(M, N, K, TM, TN, TK, 0.125, 1.5, owns=lambda pm, pn: pm == row)
+            total += pod.run(cl.segment_text(ins))["compute"]
+        assert total == (M // TM) * (N // TN) * (1 + K // TK)
+    finally:
+        pod.close()
+    _check_c(paths, M, N, K)
