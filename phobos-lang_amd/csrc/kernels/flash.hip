@@ -431,10 +431,6 @@ __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp
     const float c2 = softmax_c2(scale);
     const uint32_t nkb = (Nk + BC - 1) / BC;
     char *const S[NSTAGE] = {st0, st1, st2, st3};
-#ifdef PHX_CLOCK_PROBE  // measurement-only build: never built by the Makefile
-    const uint64_t probe_t0 = __builtin_amdgcn_s_memtime();
-    const uint64_t probe_r0 = __builtin_amdgcn_s_memrealtime();
-#endif
 
     // per-lane source offsets of the LDS copies (see dma_block): the K
     // swizzle depends on bit 2 of the row, i.e. on the wave's parity
@@ -506,15 +502,6 @@ __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp
                 *(phx_h4 *)(orow + 32 * dt + 8 * b + 4 * g) = v;
             }
     }
-#ifdef PHX_CLOCK_PROBE
-    // shader-clock and 100 MHz spans of this wave, /64, over O[qw][0..1]
-    const uint64_t probe_t1 = __builtin_amdgcn_s_memtime();
-    const uint64_t probe_r1 = __builtin_amdgcn_s_memrealtime();
-    if (lane == 0 && qw < Nq) {
-        O[(int64_t)qw * ldo] = (_Float16)((float)(probe_t1 - probe_t0) / 64);
-        O[(int64_t)qw * ldo + 1] = (_Float16)((float)(probe_r1 - probe_r0) / 64);
-    }
-#endif
 }
 #else
 // ---------------------------------------------------------------- f32 path

@@ -557,11 +557,6 @@ __device__ __forceinline__ void gemm_body(const TIn *A, const TIn *B, TOut *C, i
         (uint32_t)(((lane >> 5) * ldb + 8 * ((lane & 31) ^ (4 * (2 + (lane >> 5))))) * 2);
 #endif
 
-#ifdef PHX_CLOCK_PROBE
-    const uint64_t probe_t0 = __builtin_amdgcn_s_memtime();
-    const uint64_t probe_r0 = __builtin_amdgcn_s_memrealtime();
-    uint32_t probe_m0 = ~0u, probe_n0 = 0;
-#endif
     for (uint32_t t = phx_block_linear(); t < ntiles; t += nblk) {
         const uint32_t ts = nblk == ntiles ? phx_xcd_swizzle(t, ntiles) : t;
         const uint32_t gsz = GROUP_M * tiles_n;
@@ -570,10 +565,6 @@ __device__ __forceinline__ void gemm_body(const TIn *A, const TIn *B, TOut *C, i
         const uint32_t tm = g0 + (ts % gsz) % gm;
         const uint32_t tn = (ts % gsz) / gm;
         const uint32_t m0 = tm * BM, n0 = tn * BN;
-#ifdef PHX_CLOCK_PROBE
-        probe_m0 = m0;
-        probe_n0 = n0;
-#endif
 
         phx_f16v acc[4][4];
 #pragma unroll
@@ -643,16 +634,6 @@ __device__ __forceinline__ void gemm_body(const TIn *A, const TIn *B, TOut *C, i
         __syncthreads();
 #endif
     }
-#ifdef PHX_CLOCK_PROBE
-    // measurement-only build: overwrite two outputs with this workgroup's
-    // shader-clock and 100 MHz real-time spans
-    const uint64_t probe_t1 = __builtin_amdgcn_s_memtime();
-    const uint64_t probe_r1 = __builtin_amdgcn_s_memrealtime();
-    if (tid == 0 && probe_m0 != ~0u) {  // first two outputs of this workgroup's last tile
-        C[(int64_t)probe_m0 * ldc + probe_n0] = (TOut)((float)(probe_t1 - probe_t0) / 64);
-        C[(int64_t)probe_m0 * ldc + probe_n0 + 1] = (TOut)((float)(probe_r1 - probe_r0) / 64);
-    }
-#endif
 }
 
 extern "C" __global__ __launch_bounds__(NT, 1) void gemm(PHX_MEMREF2(TIn, a, int64_t),

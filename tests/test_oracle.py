@@ -150,6 +150,42 @@ def test_fp16acc_model_close_to_f64():
         assert abs(v - want[i, j]) < 2e-2
 
 
+def _fp16acc(a_row, b_col, K, alpha=1.0, beta=0.0, c=0.0):
+    A = np.asarray(a_row, np.float32).reshape(1, K)
+    B = np.asarray(b_col, np.float32).reshape(K, 1)
+    C = np.full((1, 1), c, np.float32)
+    return oracle.gemm_fp16acc_point(0, 0, A, B, C, alpha, beta)
+
+
+def test_fp16acc_model_known_answers():
+    """Known answers of main.rs:663-670's model (f16 accumulator rounded after
+    every step, product and sum in f32, epilogue f16(alpha*acc + beta*c)),
+    each chosen so that an f32-accumulating or product-rounding variant fails."""
+    # 4096 ones: the f16 running sum stops at 2048 (2048 + 1 is a tie that
+    # rounds to the even 2048); an f32 accumulator would give 4096.
+    K = 4096
+    assert _fp16acc(np.ones(K), np.ones(K), K) == 2048.0
+    assert float(np.ones(K, np.float32).sum()) == 4096.0
+    # 2048 + 1 + 1 stays 2048, whatever the order of the ones after it.
+    assert _fp16acc([2048.0, 1.0, 1.0], [1.0, 1.0, 1.0], 3) == 2048.0
+    assert _fp16acc([1.0, 1.0, 2048.0], [1.0, 1.0, 1.0], 3) == 2050.0
+    # The product is added unrounded: (1+2^-10) + (1+2^-10)(1+3*2^-10) =
+    # 2 + 5*2^-10 + 3*2^-20 is just above a tie and rounds up to 2 + 6*2^-10.
+    # Rounding the product to f16 first (1 + 2^-8) lands on the tie itself,
+    # which rounds to the even 2 + 4*2^-10.
+    u = 2.0**-10
+    assert _fp16acc([1 + u, 1 + u], [1.0, 1 + 3 * u], 2) == 2 + 6 * u
+    assert float(np.float16(np.float32(1 + u) + np.float32(np.float16((1 + u) * (1 + 3 * u))))) \
+        == 2 + 4 * u
+    # Inputs are rounded to f16 (RNE) before the product: 1 + 2^-12 -> 1.
+    assert _fp16acc([1.0 + 2.0**-12], [3.0], 1) == 3.0
+    # Epilogue: f16(fl(alpha*acc) + fl(beta*c)); 0.5*2048 + 0.25*4 = 1025 is
+    # exact in f16, 1024 + 0.5 (beta*c = 0.5) is a tie that rounds to 1024.
+    assert _fp16acc([2048.0], [1.0], 1, 0.5, 0.25, 4.0) == 1025.0
+    assert _fp16acc([2048.0], [1.0], 1, 0.5, 0.25, 2.0) == 1024.0
+    assert _fp16acc([2048.0], [1.0], 1, 0.5, 0.25, 2.0 + 2.0**-10) == 1025.0
+
+
 # ---------------------------------------------------------------- flash
 def _softmax_attention(q, k, v, scale):
     s = q.astype(np.float64) @ k.astype(np.float64).T * scale
