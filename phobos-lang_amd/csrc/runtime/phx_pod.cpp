@@ -950,6 +950,7 @@ static int run_instrs(phx_pod p, std::vector<Instr> &ins, uint64_t stats[8]) {
         *out = &it->second;
         return PHX_OK;
     };
+    std::vector<uint64_t> allocated_here;  // released again if the segment fails
     auto region_ok = [&](const Instr &I, const TileBuf &tb, const TensorInfo &ti) -> int {
         uint64_t elems = 1;
         for (auto s : I.region.shape) elems *= s;
@@ -958,7 +959,16 @@ static int run_instrs(phx_pod p, std::vector<Instr> &ins, uint64_t stats[8]) {
                              (unsigned long long)elems, tb.elems);
         if (I.region.shape.size() != ti.shape.size() && !(I.region.shape.size() == 1))
             return set_error(PHX_E_SEGMENT, "region rank != tensor rank");
-        for (size_t d = 0; d < I.region.shape.size() && d < ti.shape.size(); ++d)
+        if (I.region.shape.size() == 1 && ti.shape.size() > 1) {
+            // a rank-1 region over a higher-rank tensor is a flat element
+            // range, as byte_spans reads it (storage.rs:22-79)
+            uint64_t total = 1;
+            for (auto s : ti.shape) total *= s;
+            if (I.region.offset[0] + I.region.shape[0] > total)
+                return set_error(PHX_E_SEGMENT, "region exceeds tensor bounds");
+            return PHX_OK;
+        }
+        for (size_t d = 0; d < I.region.shape.size(); ++d)
             if (I.region.offset[d] + I.region.shape[d] > ti.shape[d])
                 return set_error(PHX_E_SEGMENT, "region exceeds tensor bounds");
         return PHX_OK;
@@ -981,6 +991,7 @@ static int run_instrs(phx_pod p, std::vector<Instr> &ins, uint64_t stats[8]) {
             tb.shape = I.shape;
             tb.elems = elems;
             p->tiles[I.tile] = tb;
+            allocated_here.push_back(I.tile);
             st[0]++;
             complete(i);
             return PHX_OK;
@@ -1126,14 +1137,24 @@ static int run_instrs(phx_pod p, std::vector<Instr> &ins, uint64_t stats[8]) {
             Inflight fl{Inflight::Kernel, i};
             hipError_t e;
             if ((e = hipEventCreate(&fl.start)) != hipSuccess) return hip_error(e, "hipEventCreate");
-            if ((e = hipEventCreate(&fl.done)) != hipSuccess) return hip_error(e, "hipEventCreate");
-            if ((e = hipEventRecord(fl.start, s)) != hipSuccess) return hip_error(e, "hipEventRecord");
+            if ((e = hipEventCreate(&fl.done)) != hipSuccess) {
+                (void)hipEventDestroy(fl.start);
+                return hip_error(e, "hipEventCreate");
+            }
+            if ((e = hipEventRecord(fl.start, s)) != hipSuccess) {
+                (void)hipEventDestroy(fl.start);
+                (void)hipEventDestroy(fl.done);
+                return hip_error(e, "hipEventRecord");
+            }
             if (int rc = phx_compute((phx_function)f, bits, targs.data(), (uint32_t)targs.size(),
                                      I.scalars.data(), (uint32_t)I.scalars.size(), grid, block,
-                                     (phx_stream)s))
+                                     (phx_stream)s)) {
+                (void)hipEventDestroy(fl.start);
+                (void)hipEventDestroy(fl.done);
                 return rc;
+            }
+            inflight.push_back(fl);  // the error drain destroys its events from here on
             if ((e = hipEventRecord(fl.done, s)) != hipSuccess) return hip_error(e, "hipEventRecord");
-            inflight.push_back(fl);
             return PHX_OK;
         }
         }
@@ -1156,13 +1177,16 @@ static int run_instrs(phx_pod p, std::vector<Instr> &ins, uint64_t stats[8]) {
             std::lock_guard<std::mutex> l(io_mu);
             done.swap(io_done);
         }
+        // every entry taken is accounted for before any is acted on, so an
+        // error part-way through the batch still lets io_pending reach 0
+        io_pending -= done.size();
         for (auto &d : done) {
-            io_pending--;
             st[7] += d.ns;
             progress = true;
-            if (!d.ok) {
-                err = set_error(PHX_E_IO, "%s", d.err.c_str());
-                break;
+            if (err || !d.ok) {
+                if (d.staging) put_pinned(d.staging, d.bytes);  // STORE: the write is over
+                if (!err) err = set_error(PHX_E_IO, "%s", d.err.c_str());
+                continue;
             }
             Instr &I = ins[d.idx];
             if (I.kind == OpKind::Load) {
@@ -1178,6 +1202,7 @@ static int run_instrs(phx_pod p, std::vector<Instr> &ins, uint64_t stats[8]) {
                         if (e != hipSuccess) err = hip_error(e, "LOAD hipMemcpyAsync");
                         break;
                     }
+                if (err) continue;
             } else {  // STORE finished writing the file
                 put_pinned(d.staging, d.bytes);
                 st[3]++;
@@ -1271,13 +1296,16 @@ static int run_instrs(phx_pod p, std::vector<Instr> &ins, uint64_t stats[8]) {
             std::this_thread::sleep_for(std::chrono::microseconds(20));
         }
     }
-    // drain: never leave work in flight that references this call's state
+    // drain: never leave work in flight that references this call's state,
+    // then hand back what the call took, so the pod can run a segment again
     if (err) {
         for (auto s : p->streams) (void)hipStreamSynchronize(s);
         (void)hipStreamSynchronize(p->copy_stream);
         for (;;) {
             {
                 std::lock_guard<std::mutex> l(io_mu);
+                for (auto &d : io_done)
+                    if (d.staging) put_pinned(d.staging, d.bytes);
                 io_pending -= io_done.size();
                 io_done.clear();
             }
@@ -1287,6 +1315,13 @@ static int run_instrs(phx_pod p, std::vector<Instr> &ins, uint64_t stats[8]) {
         for (auto &f : inflight) {
             if (f.start) (void)hipEventDestroy(f.start);
             if (f.done) (void)hipEventDestroy(f.done);
+            if (f.staging) put_pinned(f.staging, f.staging_bytes);
+        }
+        for (uint64_t id : allocated_here) {
+            auto it = p->tiles.find(id);
+            if (it == p->tiles.end()) continue;
+            phx_arena_free(p->arena, it->second.addr, it->second.cls);
+            p->tiles.erase(it);
         }
         return err;
     }

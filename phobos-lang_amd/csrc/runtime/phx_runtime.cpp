@@ -7,6 +7,7 @@
 
 #include <dlfcn.h>
 
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -62,10 +63,26 @@ struct State {
     int device = -1;
     std::string dir;
     std::unordered_map<std::string, hipModule_t> modules;  // file -> module
-    hipFunction_t fns[PHX_NUM_KERNELS] = {};
+    // written under mu by builtin(), read without it by launch_raw()
+    std::atomic<hipFunction_t> fns[PHX_NUM_KERNELS] = {};
+    // Functions a caller got from its own load of a built-in code object
+    // file (phx_module_load_file + phx_module_get_function), keyed to the
+    // built-in they are; under mu.
+    std::unordered_map<hipModule_t, std::string> module_files;  // module -> file name
+    std::unordered_map<hipFunction_t, std::pair<int, hipModule_t>> aliases;
     std::mutex mu;
 };
 static State g;
+
+// The built-in kernel id `f` is, or -1.
+static int builtin_id(hipFunction_t f) {
+    if (!f) return -1;
+    for (int k = 0; k < PHX_NUM_KERNELS; ++k)
+        if (g.fns[k].load(std::memory_order_acquire) == f) return k;
+    std::lock_guard<std::mutex> lock(g.mu);
+    auto it = g.aliases.find(f);
+    return it == g.aliases.end() ? -1 : it->second.first;
+}
 
 static std::string default_dir() {
     if (const char *env = getenv("PHX_CODE_OBJECT_DIR")) return env;
@@ -87,8 +104,12 @@ int builtin(phx_kernel k, hipFunction_t *out) {
     if (int rc = ensure_init()) return rc;
     if ((int)k < 0 || k >= PHX_NUM_KERNELS)
         return set_error(PHX_E_INVALID, "unknown kernel id %d", (int)k);
+    if (hipFunction_t f = g.fns[k].load(std::memory_order_acquire)) {
+        *out = f;
+        return PHX_OK;
+    }
     std::lock_guard<std::mutex> lock(g.mu);
-    if (!g.fns[k]) {
+    if (!g.fns[k].load(std::memory_order_relaxed)) {
         const KernelSpec &s = kSpecs[k];
         hipModule_t mod;
         auto it = g.modules.find(s.file);
@@ -108,9 +129,9 @@ int builtin(phx_kernel k, hipFunction_t *out) {
         if (e != hipSuccess)
             return set_error(PHX_E_NOT_FOUND, "entry '%s' not in %s: %s", s.entry, s.file,
                              hipGetErrorString(e));
-        g.fns[k] = f;
+        g.fns[k].store(f, std::memory_order_release);
     }
-    *out = g.fns[k];
+    *out = g.fns[k].load(std::memory_order_relaxed);
     return PHX_OK;
 }
 
@@ -159,20 +180,153 @@ struct ArgPack {
     }
 };
 
+// ------------------------------------------------------------------ raw launches
+// One exploded-memref descriptor read back out of a void** argument list.
+struct Desc {
+    uint64_t ptr = 0;  // aligned pointer + offset, in bytes
+    int64_t size[3] = {0, 0, 0};
+    int64_t stride[3] = {0, 0, 0};
+};
+
+static int64_t arg_idx(void **args, int i, int bits) {
+    if (bits == 32) {
+        int32_t v;
+        memcpy(&v, args[i], 4);
+        return v;
+    }
+    int64_t v;
+    memcpy(&v, args[i], 8);
+    return v;
+}
+
+// Reads `n` rank-`rank` descriptors starting at args[0]; `esz` is the element
+// size the offset is scaled by.
+static void read_descs(void **args, int n, int rank, int bits, int esz, Desc *d) {
+    int a = 0;
+    for (int t = 0; t < n; ++t) {
+        uint64_t aligned;
+        memcpy(&aligned, args[a + 1], 8);
+        d[t].ptr = aligned + (uint64_t)(arg_idx(args, a + 2, bits) * esz);
+        for (int r = 0; r < rank; ++r) d[t].size[r] = arg_idx(args, a + 3 + r, bits);
+        for (int r = 0; r < rank; ++r) d[t].stride[r] = arg_idx(args, a + 3 + rank + r, bits);
+        a += 3 + 2 * rank;
+    }
+}
+
+// The problem extents of a built-in kernel's launch, read from its argument
+// list the way the kernel reads them, after the same consistency checks the
+// kernel makes on entry (a launch that fails them would return without
+// output, so it is refused here instead).
+static int builtin_dims(phx_kernel k, void **args, int64_t *d, int *nd) {
+    if (!args) return set_error(PHX_E_INVALID, "%s: null argument list", kSpecs[k].entry);
+    const int bits = kSpecs[k].index_bits;
+    Desc t[4];
+    auto bad = [&](const char *why) {
+        return set_error(PHX_E_INVALID, "%s (%s): %s", kSpecs[k].entry, kSpecs[k].file, why);
+    };
+    switch (k) {
+    case PHX_SAXPY_FP32:
+        read_descs(args, 3, 1, bits, 4, t);
+        if (t[1].size[0] != t[0].size[0] || t[2].size[0] != t[0].size[0])
+            return bad("x, y and out differ in length");
+        if (t[0].size[0] > 0 && (!t[0].ptr || !t[1].ptr || !t[2].ptr)) return bad("null operand");
+        d[0] = t[0].size[0];
+        *nd = 1;
+        return PHX_OK;
+    case PHX_GEMM_FP32:
+    case PHX_GEMM_FP16TC_FP32ACC:
+    case PHX_GEMM_FP16:
+    case PHX_MATMUL: {
+        read_descs(args, 3, 2, bits, k == PHX_GEMM_FP16 ? 2 : 4, t);
+        const int64_t M = t[0].size[0], K = t[0].size[1], N = t[1].size[1];
+        if (t[1].size[0] != K || t[2].size[0] != M || t[2].size[1] != N)
+            return bad("A, B and C extents do not chain as [M,K] x [K,N] -> [M,N]");
+        for (int i = 0; i < 3; ++i)
+            if (t[i].stride[1] != 1) return bad("operands need a unit minor stride");
+        const int nm = k == PHX_GEMM_FP16 ? PHX_H16_NK_MULT
+                       : k == PHX_GEMM_FP16TC_FP32ACC ? PHX_TC_N_MULT : PHX_S_NK_MULT;
+        const int km = k == PHX_GEMM_FP16TC_FP32ACC ? PHX_TC_K_MULT : nm;
+        if (t[0].stride[0] % km || t[1].stride[0] % nm || t[2].stride[0] % nm)
+            return bad("row strides must keep every row 16-byte aligned");
+        if (!t[0].ptr || !t[1].ptr || !t[2].ptr) return bad("null operand");
+        if ((t[0].ptr | t[1].ptr | t[2].ptr) & 15) return bad("operands must be 16-byte aligned");
+        d[0] = M;
+        d[1] = N;
+        d[2] = K;
+        *nd = 3;
+        return PHX_OK;
+    }
+    case PHX_MATMUL_INIT:
+        read_descs(args, 1, 2, bits, 4, t);
+        if (t[0].stride[1] != 1) return bad("C needs a unit minor stride");
+        if (t[0].size[0] * t[0].size[1] > 0 && !t[0].ptr) return bad("null operand");
+        d[0] = t[0].size[0];
+        d[1] = t[0].size[1];
+        *nd = 2;
+        return PHX_OK;
+    case PHX_FLASH_FP32:
+    case PHX_FLASH_FP16: {
+        read_descs(args, 4, 2, bits, k == PHX_FLASH_FP16 ? 2 : 4, t);
+        const int64_t Nq = t[0].size[0], Nk = t[1].size[0], D = t[0].size[1];
+        if (t[1].size[1] != D || t[2].size[1] != D || t[3].size[1] != D || t[2].size[0] != Nk ||
+            t[3].size[0] != Nq)
+            return bad("Q, K, V and O extents disagree");
+        for (int i = 0; i < 4; ++i)
+            if (t[i].stride[1] != 1 || t[i].stride[0] % 8)
+                return bad("operands need a unit minor stride and rows of whole 16-byte chunks");
+        if (!t[0].ptr || !t[1].ptr || !t[2].ptr || !t[3].ptr) return bad("null operand");
+        if ((t[0].ptr | t[1].ptr | t[2].ptr | t[3].ptr) & 15)
+            return bad("operands must be 16-byte aligned");
+        d[0] = Nq;
+        d[1] = Nk;
+        d[2] = D;
+        *nd = 3;
+        return PHX_OK;
+    }
+    case PHX_FLASH_FP32_BH:
+    case PHX_FLASH_FP16_BH: {
+        read_descs(args, 4, 3, bits, k == PHX_FLASH_FP16_BH ? 2 : 4, t);
+        const int64_t H = t[0].size[0], Nq = t[0].size[1], Nk = t[1].size[1], D = t[0].size[2];
+        for (int i = 1; i < 4; ++i)
+            if (t[i].size[0] != H || t[i].size[2] != D) return bad("Q, K, V and O extents disagree");
+        if (t[2].size[1] != Nk || t[3].size[1] != Nq) return bad("Q, K, V and O extents disagree");
+        for (int i = 0; i < 4; ++i)
+            if (t[i].stride[2] != 1 || (t[i].stride[0] | t[i].stride[1]) % 8)
+                return bad("operands need a unit minor stride and rows of whole 16-byte chunks");
+        if (!t[0].ptr || !t[1].ptr || !t[2].ptr || !t[3].ptr) return bad("null operand");
+        if ((t[0].ptr | t[1].ptr | t[2].ptr | t[3].ptr) & 15)
+            return bad("operands must be 16-byte aligned");
+        d[0] = H;
+        d[1] = Nq;
+        d[2] = Nk;
+        d[3] = D;
+        *nd = 4;
+        return PHX_OK;
+    }
+    default:
+        return set_error(PHX_E_INVALID, "unknown kernel id %d", (int)k);
+    }
+}
+
 int launch_raw(hipFunction_t f, const uint32_t grid[3], const uint32_t block[3], uint32_t shmem,
                hipStream_t s, void **args) {
-    // The built-in kernels are written for one workgroup size and do nothing
-    // at any other (they check blockDim on entry): reject such a launch here
-    // rather than let it return without output.
-    for (int k = 0; k < PHX_NUM_KERNELS; ++k) {
-        if (!g.fns[k] || g.fns[k] != f) continue;
-        if (block[0] != kSpecs[k].block || block[1] != 1 || block[2] != 1)
-            return set_error(PHX_E_INVALID,
-                             "%s (%s) runs with a workgroup of (%u,1,1) threads, got (%u,%u,%u); "
-                             "see phx_kernel_abi", kSpecs[k].entry, kSpecs[k].file,
-                             kSpecs[k].block, block[0], block[1], block[2]);
-        break;
+    // A built-in kernel runs on this backend's own tiling, whatever geometry
+    // the caller derived from the reference's tiles (e.g. saxpy's 1024-thread
+    // blocks, flash's @launch(128)): its grid and workgroup come from
+    // grid_for() over the extents in its own argument list.  The kernels
+    // need no dynamic LDS, so the shared-memory size is ignored as well.
+    if (int k = builtin_id(f); k >= 0) {
+        int64_t d[4];
+        int nd = 0;
+        if (int rc = builtin_dims((phx_kernel)k, args, d, &nd)) return rc;
+        uint32_t g2[3], b2[3];
+        if (int rc = grid_for((phx_kernel)k, d, nd, g2, b2)) return rc;
+        hipError_t e = hipModuleLaunchKernel(f, g2[0], g2[1], g2[2], b2[0], b2[1], b2[2], 0, s,
+                                             args, nullptr);
+        if (e != hipSuccess) return hip_error(e, "hipModuleLaunchKernel");
+        return PHX_OK;
     }
+    if (!grid || !block) return set_error(PHX_E_INVALID, "null grid or block");
     hipError_t e = hipModuleLaunchKernel(f, grid[0], grid[1], grid[2], block[0], block[1],
                                          block[2], shmem, s, args, nullptr);
     if (e != hipSuccess) return hip_error(e, "hipModuleLaunchKernel");
@@ -329,7 +483,7 @@ int phx_shutdown(void) {
     std::lock_guard<std::mutex> lock(g.mu);
     for (auto &kv : g.modules) (void)hipModuleUnload(kv.second);
     g.modules.clear();
-    for (auto &f : g.fns) f = nullptr;
+    for (auto &f : g.fns) f.store(nullptr, std::memory_order_release);
     g.init = false;
     return PHX_OK;
 }
@@ -465,9 +619,18 @@ int phx_module_load_file(phx_module *m, const char *path) {
     hipError_t e = hipModuleLoad(&h, path);
     if (e != hipSuccess) return hip_error(e, "hipModuleLoad");
     *m = (phx_module)h;
+    const char *base = strrchr(path, '/');
+    std::lock_guard<std::mutex> lock(g.mu);
+    g.module_files[h] = base ? base + 1 : path;
     return PHX_OK;
 }
 int phx_module_unload(phx_module m) {
+    {
+        std::lock_guard<std::mutex> lock(g.mu);
+        g.module_files.erase((hipModule_t)m);
+        for (auto it = g.aliases.begin(); it != g.aliases.end();)
+            it = it->second.second == (hipModule_t)m ? g.aliases.erase(it) : std::next(it);
+    }
     hipError_t e = hipModuleUnload((hipModule_t)m);
     return e == hipSuccess ? PHX_OK : hip_error(e, "hipModuleUnload");
 }
@@ -476,6 +639,14 @@ int phx_module_get_function(phx_function *f, phx_module m, const char *name) {
     hipError_t e = hipModuleGetFunction(&h, (hipModule_t)m, name);
     if (e != hipSuccess) return set_error(PHX_E_NOT_FOUND, "entry '%s': %s", name, hipGetErrorString(e));
     *f = (phx_function)h;
+    // a caller's own load of a built-in code object gets the built-in's
+    // launch geometry too (see launch_raw)
+    std::lock_guard<std::mutex> lock(g.mu);
+    auto it = g.module_files.find((hipModule_t)m);
+    if (it != g.module_files.end())
+        for (int k = 0; k < PHX_NUM_KERNELS; ++k)
+            if (it->second == kSpecs[k].file && strcmp(name, kSpecs[k].entry) == 0)
+                g.aliases[h] = {k, (hipModule_t)m};
     return PHX_OK;
 }
 int phx_builtin_function(phx_function *f, phx_kernel k) {

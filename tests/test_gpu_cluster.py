@@ -279,3 +279,60 @@ def test_job_split_into_segments_under_a_small_arena(px_gpu, tmp_path):
     finally:
         pod.close()
     _check_c(paths, M, N, K)
+
+
+def test_io_errors_return_promptly_and_release_the_segment(px_gpu, tmp_path):
+    # Eight LOADs of a file that does not exist finish on the I/O pool at
+    # about the same time.  The segment fails with PHX_E_IO without waiting
+    # on them forever, and gives back its tiles and staging: the same pod
+    # then runs a good segment that reuses the tile ids.
+    import time
+    px = px_gpu
+    n = 1024
+    good = str(tmp_path / "good.bin")
+    out = str(tmp_path / "out.bin")
+    x = oracle.lcg_f32(7, n)
+    x.tofile(good)
+    np.zeros(n, np.float32).tofile(out)
+    pod = cl.Pod(64 << 20, nstreams=2)
+    pod.set_tensor(0, "file://" + str(tmp_path / "missing.bin"), (n,))
+    pod.set_tensor(1, "file://" + good, (n,))
+    pod.set_tensor(2, "file://" + out, (n,))
+    bad = [f"{i} - ALLOC {100 + i} {n} f32" for i in range(1, 9)]
+    bad += [f"{10 + i} {i} LOAD {100 + i} 0 0 {n}" for i in range(1, 9)]
+    t0 = time.monotonic()
+    with pytest.raises(px.PhxError) as e:
+        pod.run("\n".join(bad) + "\n")
+    assert time.monotonic() - t0 < 10
+    assert e.value.code == 1005 and "missing.bin" in str(e.value)
+    seg = "\n".join(["1 - ALLOC 101 1024 f32", "2 1 LOAD 101 1 0 1024",
+                     "3 2 STORE 101 2 0 1024", "4 3 FREE 101 0"]) + "\n"
+    stats = pod.run(seg)
+    assert stats["load"] == 1 and stats["store"] == 1
+    assert np.array_equal(np.fromfile(out, np.float32).view(np.uint32), x.view(np.uint32))
+    pod.close()
+
+
+def test_flat_region_over_a_2d_tensor(px_gpu, tmp_path):
+    # A rank-1 region over a rank-2 tensor is a flat element range
+    # (storage.rs:22-79 byte_spans): 0..R*C covers the whole tensor, and an
+    # offset of half the elements the second half.
+    R, C = 32, 32
+    src, dst = str(tmp_path / "src.bin"), str(tmp_path / "dst.bin")
+    x = oracle.lcg_f32(8, R * C)
+    x.tofile(src)
+    np.zeros(R * C, np.float32).tofile(dst)
+    pod = cl.Pod(16 << 20, nstreams=1)
+    pod.set_tensor(0, "file://" + src, (R, C))
+    pod.set_tensor(1, "file://" + dst, (R, C))
+    half = R * C // 2
+    seg = "\n".join([
+        f"1 - ALLOC 201 {R * C} f32", f"2 - ALLOC 202 {half} f32",
+        f"3 1 LOAD 201 0 0 {R * C}", f"4 2 LOAD 202 0 {half} {half}",
+        f"5 3 STORE 201 1 0 {R * C}", f"6 4,5 STORE 202 1 0 {half}",
+        "7 6 FREE 201 0", "8 6 FREE 202 0"]) + "\n"
+    pod.run(seg)
+    got = np.fromfile(dst, np.float32)
+    want = np.concatenate([x[half:], x[half:]])
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    pod.close()

@@ -27,8 +27,8 @@ def test_module_load_data_and_raw_launch_saxpy(px_gpu, stream):
     x, y = oracle.lcg_f32(1, n), oracle.lcg_f32(2, n)
     dx, dy = px.DeviceBuffer.from_array(x), px.DeviceBuffer.from_array(y)
     do = px.DeviceBuffer(n * 4)
-    # the reference's own geometry: BLOCK=16 -> grid ceil(n/16), 1024 threads is
-    # not this kernel's block; use the grid the reference would pick with our block.
+    # a module loaded from bytes is the caller's own kernel to the backend:
+    # it launches with the caller's geometry, here grid ceil(n/16), 256 threads
     px.compute(fn.value, 32, [(dx.ptr, (n,)), (dy.ptr, (n,)), (do.ptr, (n,))],
                [(3, 4, px.f32_bits(2.5))], ((n + 15) // 16, 1, 1), (256, 1, 1), stream)
     stream.synchronize()
@@ -159,6 +159,37 @@ def test_launch_by_reference_names_with_void_args(px_gpu, stream):
     stream.synchronize()
     want = oracle.saxpy(np.float32(2.5), x, y)
     assert np.array_equal(do.download(np.float32, n).view(np.uint32), want.view(np.uint32))
+    # the reference bench's own geometry (main.rs:1216-1235): grid
+    # ceil(n/BLOCK) with BLOCK = 16 and 1024-thread blocks; the backend runs
+    # saxpy on its own geometry, with y aliased as out (y = alpha*x + y)
+    dy2 = px.DeviceBuffer.from_array(y)
+    vals2 = []
+    for b in (dx, dy2, dy2):
+        vals2 += [ctypes.c_void_p(b.ptr), ctypes.c_void_p(b.ptr), ctypes.c_int32(0),
+                  ctypes.c_int32(n), ctypes.c_int32(1)]
+    vals2.append(ctypes.c_float(2.5))
+    args2 = (ctypes.c_void_p * len(vals2))(*[ctypes.cast(ctypes.pointer(v), ctypes.c_void_p)
+                                             for v in vals2])
+    grid2 = (ctypes.c_uint32 * 3)((n + 15) // 16, 1, 1)
+    block2 = (ctypes.c_uint32 * 3)(1024, 1, 1)
+    assert px.lib().phx_launch_by_name(b"saxpy_fp32", b"saxpy", grid2, block2, stream.handle,
+                                       args2) == 0
+    # and through the caller's own load of the code object file, as
+    # Module::from_ptx + get_function would
+    m = ctypes.c_void_p()
+    px.check(px.lib().phx_module_load_file(ctypes.byref(m),
+                                           os.path.join(px.LIB_DIR, "saxpy_fp32.hsaco").encode()))
+    fn = ctypes.c_void_p()
+    px.check(px.lib().phx_module_get_function(ctypes.byref(fn), m, b"saxpy"))
+    do3 = px.DeviceBuffer(n * 4)
+    vals3 = vals2[:10] + [ctypes.c_void_p(do3.ptr), ctypes.c_void_p(do3.ptr), ctypes.c_int32(0),
+                          ctypes.c_int32(n), ctypes.c_int32(1), ctypes.c_float(2.5)]
+    args3 = (ctypes.c_void_p * len(vals3))(*[ctypes.cast(ctypes.pointer(v), ctypes.c_void_p)
+                                             for v in vals3])
+    px.check(px.lib().phx_launch(fn, grid2, block2, 0, stream.handle, args3))
+    stream.synchronize()
+    assert np.array_equal(dy2.download(np.float32, n).view(np.uint32), want.view(np.uint32))
+    px.check(px.lib().phx_module_unload(m))
     # unknown names are refused before any launch
     assert px.lib().phx_launch_by_name(b"gemm_fp64", b"gemm", grid, None, stream.handle, args) \
         == px.PHX_E_INVALID

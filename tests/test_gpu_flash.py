@@ -186,15 +186,61 @@ def test_flash_block_sum_over_limit_without_raise(px_gpu, stream, bits):
     assert _rel(got, want) < TOL[bits]
 
 
-def test_launch_with_wrong_workgroup_size_is_rejected(px_gpu, stream):
-    # flash_fp16 runs 512-thread workgroups; a raw launch with the reference's
-    # cta, or any other size, is refused on the host instead of running a
-    # kernel that would return without output.
+def _void_args(vals):
+    import ctypes
+    return vals, (ctypes.c_void_p * len(vals))(
+        *[ctypes.cast(ctypes.pointer(v), ctypes.c_void_p) for v in vals])
+
+
+@pytest.mark.parametrize("bits", [16, 32])
+def test_flash_with_reference_bench_geometry(px_gpu, stream, bits):
+    # launch_flash (main.rs:334-371): grid Nq/BR with the reference's BR, the
+    # @launch(128) cta, i64 exploded memrefs, one head.  The backend replaces
+    # grid and cta with its own; the result equals the typed launch bit for
+    # bit and the oracle within the kernel's tolerance.
+    import ctypes
     px = px_gpu
-    BH, N, D = 1, 256, 64
-    bufs = [px.DeviceBuffer(BH * N * D * 2) for _ in range(4)]
-    fn = px.builtin_function(px.FLASH_FP16_BH)
-    with pytest.raises(px.PhxError) as e:
-        px.compute(fn, 64, [(b.ptr, (BH, N, D)) for b in bufs], [(4, 4, px.f32_bits(0.125))],
-                   (1, 1, 1), (256, 1, 1), stream)
-    assert e.value.code == px.PHX_E_INVALID and "phx_kernel_abi" in str(e.value)
+    Nq, Nk, D = 512, 384, 64
+    q, k, v = _inputs((Nq, D), bits, 61)[0], *_inputs((Nk, D), bits, 62)[1:]
+    dq, dk, dv = (_upload(px, t, bits) for t in (q, k, v))
+    esz = 2 if bits == 16 else 4
+    do, dr = px.DeviceBuffer(Nq * D * esz), px.DeviceBuffer(Nq * D * esz)
+    vals = []
+    for buf, n in ((dq, Nq), (dk, Nk), (dv, Nk), (do, Nq)):
+        vals += [ctypes.c_void_p(buf.ptr), ctypes.c_void_p(buf.ptr), ctypes.c_int64(0),
+                 ctypes.c_int64(n), ctypes.c_int64(D), ctypes.c_int64(D), ctypes.c_int64(1)]
+    vals.append(ctypes.c_float(0.125))
+    keep, args = _void_args(vals)
+    stem = b"flash_attention_fp16" if bits == 16 else b"flash_attention_fp32"
+    grid = (ctypes.c_uint32 * 3)(Nq // 64, 1, 1)
+    block = (ctypes.c_uint32 * 3)(128, 1, 1)
+    px.check(px.lib().phx_launch_by_name(stem, b"flash_attention", grid, block, stream.handle,
+                                         args))
+    kern = px.FLASH_FP16 if bits == 16 else px.FLASH_FP32
+    px.launch_flash(stream, kern, dq.ptr, dk.ptr, dv.ptr, dr.ptr, Nq, Nk, D, 0.125)
+    stream.synchronize()
+    dt = np.uint16 if bits == 16 else np.uint32
+    assert np.array_equal(do.download(dt, Nq * D), dr.download(dt, Nq * D))
+    got = _download(do, (Nq, D), bits)
+    assert _rel(got, oracle.flash_rows(np.arange(Nq), q, k, v, 0.125)) < TOL[bits]
+
+
+def test_raw_launch_refuses_inconsistent_descriptors(px_gpu, stream):
+    # A built-in launched with descriptors the kernel would refuse on entry
+    # (here K's head dim differs from Q's) is refused on the host.
+    import ctypes
+    px = px_gpu
+    bufs = [px.DeviceBuffer(256 * 64 * 2) for _ in range(4)]
+    vals = []
+    for i, b in enumerate(bufs):
+        d = 32 if i == 1 else 64
+        vals += [ctypes.c_void_p(b.ptr), ctypes.c_void_p(b.ptr), ctypes.c_int64(0),
+                 ctypes.c_int64(256), ctypes.c_int64(d), ctypes.c_int64(d), ctypes.c_int64(1)]
+    vals.append(ctypes.c_float(0.125))
+    keep, args = _void_args(vals)
+    grid = (ctypes.c_uint32 * 3)(4, 1, 1)
+    block = (ctypes.c_uint32 * 3)(128, 1, 1)
+    rc = px.lib().phx_launch_by_name(b"flash_attention_fp16", b"flash_attention", grid, block,
+                                     stream.handle, args)
+    assert rc == px.PHX_E_INVALID and "disagree" in px.lib().phx_last_error().decode()
+    stream.synchronize()
