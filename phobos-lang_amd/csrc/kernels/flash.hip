@@ -242,7 +242,10 @@ __device__ __forceinline__ void dma_block(char *dst, const T *Kp, const T *Vp, i
 
 struct Flash16 {
     phx_f16v acc[2];  // [d tile]: d = 32dt + 8(r/4) + 4g + r%4, query lq
-    float m2, l;      // running max (log2 units) and row sum of the lane's query
+    float m2;         // running max (log2 units) of the lane's query
+    float l;          // row sum over this lane's half of the keys; lanes l and
+                      // l^32 hold the two halves of one query's sum, which
+                      // are added once, after the last block
     phx_h8 qf[4];     // Q^T operand, d slice s: d = 16s + 8g .. +7
 };
 
@@ -311,6 +314,15 @@ __device__ __forceinline__ void pv(phx_f16v (&acc)[2], const char *Vs, const phx
     __builtin_amdgcn_sched_barrier(0);
 }
 
+// The sum of a packed f16 pair in f32, starting a dot2 chain: the VOP3 form
+// of v_dot2_f32_f16 with an inline-constant zero addend.  (From a zero
+// variable the compiler emits a v_mov of the zero plus the in-place v_dot2c.)
+__device__ __forceinline__ float dot2_first(phx_h2 pp) {
+    float r;
+    asm("v_dot2_f32_f16 %0, %1, %2, 0" : "=v"(r) : "v"(pp), "s"(0x3c003c00u));  // (1, 1)
+    return r;
+}
+
 // exp2(s*c2 - m2) as f16 MFMA operands pf[c] (keys 16c + ...), and the f32
 // sum of the f16 values (v_dot2_f32_f16 against (1, 1)).
 __device__ __forceinline__ float softmax_p(phx_h8 (&pf)[4], const phx_f16v (&s)[2], float c2,
@@ -320,13 +332,12 @@ __device__ __forceinline__ float softmax_p(phx_h8 (&pf)[4], const phx_f16v (&s)[
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
         phx_h8 v;
-        part[c] = 0.0f;
 #pragma unroll
         for (int j = 0; j < 8; j += 2) {
             const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[c >> 1][8 * (c & 1) + j], c2, -m2));
             const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[c >> 1][8 * (c & 1) + j + 1], c2, -m2));
             const phx_h2 pp = {(_Float16)p0, (_Float16)p1};
-            part[c] = __builtin_amdgcn_fdot2(pp, ones, part[c], false);
+            part[c] = j == 0 ? dot2_first(pp) : __builtin_amdgcn_fdot2(pp, ones, part[c], false);
             v[j] = pp.x;
             v[j + 1] = pp.y;
         }
@@ -368,7 +379,7 @@ __device__ __forceinline__ void flash16_step(Flash16 &fs, const char *cur, char 
 #pragma unroll
         for (int c = 0; c < 4; ++c) pf[c] = (phx_h8){0, 0, 0, 0, 0, 0, 0, 0};
     } else {
-        fs.l += xor32_add(ps);
+        fs.l += ps;
     }
     pv(fs.acc, cur + KV_TILE, pf, lane);
     if (slow) {
@@ -388,7 +399,7 @@ __device__ __forceinline__ void flash16_step(Flash16 &fs, const char *cur, char 
             fs.acc[1] = fs.acc[1] * corr;
         }
         fs.m2 = m2n;
-        fs.l += xor32_add(ps);
+        fs.l += ps;
         pv(fs.acc, cur + KV_TILE, pf, lane);
     }
 }
@@ -416,7 +427,7 @@ __device__ __forceinline__ void flash16_last(Flash16 &fs, const char *cur, uint3
     fs.acc[0] = fs.acc[0] * corr;
     fs.acc[1] = fs.acc[1] * corr;
     fs.m2 = m2n;
-    fs.l += xor32_add(ps);
+    fs.l += ps;
     pv(fs.acc, cur + KV_TILE, pf, lane);
 }
 
@@ -489,6 +500,7 @@ __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp
     __syncthreads();
 
     // acc[dt][r]: d = 32dt + 8(r/4) + 4g + r%4, query qw + lq.
+    fs.l = xor32_add(fs.l);  // both halves of the query's row sum
     const uint32_t q = qw + lq;
     if (q < Nq) {
         T *orow = O + (int64_t)q * ldo;
@@ -698,13 +710,10 @@ __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp
 
 #ifdef PHX_FLASH_F16
 #define FA_QB QB  // queries per workgroup
-#define FA_LDS_DECL                                                   \
-    __shared__ __attribute__((aligned(16))) char st0[STAGE_BYTES]; \
-    __shared__ __attribute__((aligned(16))) char st1[STAGE_BYTES]; \
-    __shared__ __attribute__((aligned(16))) char st2[STAGE_BYTES]; \
-    __shared__ __attribute__((aligned(16))) char st3[STAGE_BYTES];
+// one array, so every stage address is a constant offset from one base
+#define FA_LDS_DECL __shared__ __attribute__((aligned(16))) char st[NSTAGE][STAGE_BYTES];
 #define FA_CALL(Qp, Kp, Vp, Op, ldq, ldk, ldv, ldo, Nq, Nk, q0) \
-    flash_block(Qp, Kp, Vp, Op, ldq, ldk, ldv, ldo, Nq, Nk, q0, scale, st0, st1, st2, st3)
+    flash_block(Qp, Kp, Vp, Op, ldq, ldk, ldv, ldo, Nq, Nk, q0, scale, st[0], st[1], st[2], st[3])
 #else
 #define FA_QB BR
 #define FA_LDS_DECL __shared__ __attribute__((aligned(16))) char lds[2][2][TILE_BYTES];
