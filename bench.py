@@ -195,12 +195,14 @@ def setup(px, stream, wanted):
 
 
 def cpu_baseline(seconds):
-    """The oracle's f32 blocked GEMM (OpenMP) on the host cores: a bounded
-    sample of the gemm workload, 2048^3 repeated for ~`seconds`."""
+    """The CPU counterpart of the headline: the oracle's blocked f32 GEMM
+    (OpenMP, every host core) over the gemm_fp16tc_fp32acc inputs, i.e.
+    f16-valued A and B in f32 storage, at the full 4096^3 config with C = 0,
+    alpha = 1, beta = 0; repeated for about `seconds`."""
     import oracle
-    M = 2048
-    A = oracle.lcg_f32(1, M * M).reshape(M, M)
-    B = oracle.lcg_f32(2, M * M).reshape(M, M)
+    M = 4096
+    A = oracle.f16_round(oracle.normal_f32(1, M * M, 1 / 64)).reshape(M, M)
+    B = oracle.f16_round(oracle.normal_f32(2, M * M, 1 / 64)).reshape(M, M)
     C = np.zeros((M, M), np.float32)
     flop = 2 * M ** 3 + M * M
     reps, t0 = 0, time.perf_counter()
@@ -208,42 +210,52 @@ def cpu_baseline(seconds):
         oracle.sgemm_f32(1.0, A, B, 0.0, C)
         reps += 1
         el = time.perf_counter() - t0
-        if el >= seconds or reps >= 50:
+        if el >= seconds or reps >= 30:
             break
     return {"value": round(flop * reps / el / 1e12, 4), "unit": "TFLOP/s",
             "cores": oracle.num_threads(), "kind": "port",
-            "sample": f"oracle orc_sgemm_f32 (f32, blocked, OpenMP), {M}^3 x {reps} reps "
-                      f"in {el:.1f} s"}
+            "sample": f"oracle orc_sgemm_f32 (f32 FMA, blocked, OpenMP on "
+                      f"{oracle.num_threads()} threads) over the gemm_fp16tc inputs "
+                      f"(f16-valued, f32 storage), full {M}^3, {reps} reps in {el:.1f} s"}
 
 
 def cpu_other_legs():
-    """The other kernels' CPU counterparts (oracle, on the host cores) and the
-    reference-style 64-sample f64 GEMM check (main.rs:386-445), each timed on
-    a bounded sample: a few seconds in all."""
+    """The other configs' CPU counterparts (oracle, every host core) at their
+    full BASELINE sizes, plus the reference-style 64-sample f64 GEMM check
+    (main.rs:386-445)."""
     import oracle
-    out = {"nproc": os.cpu_count(), "omp_threads": oracle.num_threads()}
+    thr = oracle.num_threads()
+    out = {"nproc": os.cpu_count(), "omp_threads": thr}
     n = 4096 * 4096
     x, y = oracle.lcg_f32(1, n), oracle.lcg_f32(2, n)
+    oracle.saxpy_mt(np.float32(2.5), x, y)
     t0 = time.perf_counter()
-    for _ in range(3):
-        oracle.saxpy(np.float32(2.5), x, y)
-    el = (time.perf_counter() - t0) / 3
-    out["saxpy_fp32"] = {"value": round(12 * n / el / 1e9, 2), "unit": "GB/s", "cores": 1,
-                         "kind": "port", "sample": f"orc_saxpy (scalar, volatile product so "
-                                                   f"nothing is contracted), full n = {n}, 3 runs"}
-    heads, S, D = 16, 4096, 64
+    for _ in range(5):
+        oracle.saxpy_mt(np.float32(2.5), x, y)
+    el = (time.perf_counter() - t0) / 5
+    out["saxpy_fp32"] = {"value": round(12 * n / el / 1e9, 2), "unit": "GB/s", "cores": thr,
+                         "kind": "port", "sample": f"orc_saxpy_mt (OpenMP, mul and add "
+                                                   f"separately rounded), full n = {n}, 5 runs"}
+    M = 4096
+    A = oracle.lcg_f32(1, M * M).reshape(M, M)
+    B = oracle.lcg_f32(2, M * M).reshape(M, M)
+    C = oracle.lcg_f32(3, M * M).reshape(M, M)
+    t0 = time.perf_counter()
+    oracle.sgemm_f32(0.125, A, B, 1.5, C)
+    el = time.perf_counter() - t0
+    out["gemm_fp32"] = {"value": round((2 * M ** 3 + M * M) / el / 1e12, 4), "unit": "TFLOP/s",
+                        "cores": thr, "kind": "port",
+                        "sample": f"orc_sgemm_f32, full {M}^3, alpha 0.125, beta 1.5, "
+                                  f"in {el:.2f} s"}
+    heads, S, D = 64, 4096, 64
     q, k, v = (oracle.normal_f32(s, heads * S * D).reshape(heads, S, D) for s in (1, 2, 3))
     t0 = time.perf_counter()
     oracle.flash_f32(q, k, v, 0.125)
     el = time.perf_counter() - t0
     out["flash_fp32"] = {"value": round(4 * S * S * D * heads / el / 1e12, 4), "unit": "TFLOP/s",
-                         "cores": oracle.num_threads(), "kind": "port",
-                         "sample": f"orc_flash_f32 (f32, OpenMP), {heads} of the 64 heads "
+                         "cores": thr, "kind": "port",
+                         "sample": f"orc_flash_f32 (f32, OpenMP), all {heads} heads "
                                    f"of 4096x4096x64 in {el:.2f} s"}
-    M = 4096
-    A = oracle.lcg_f32(1, M * M).reshape(M, M)
-    B = oracle.lcg_f32(2, M * M).reshape(M, M)
-    C = oracle.lcg_f32(3, M * M).reshape(M, M)
     r, c = oracle.sample_points(M, M, 64)
     t0 = time.perf_counter()
     oracle.gemm_points(r, c, A, B, C, 0.125, 1.5)

@@ -47,6 +47,7 @@ def lib():
         L.orc_f32_to_f16_array.argtypes = [_sz, _f32p, _u16p]
         L.orc_f16_to_f32_array.argtypes = [_sz, _u16p, _f32p]
         L.orc_saxpy.argtypes = [_sz, ctypes.c_float, _f32p, _f32p, _f32p]
+        L.orc_saxpy_mt.argtypes = [_sz, ctypes.c_float, _f32p, _f32p, _f32p]
         L.orc_sample_points.argtypes = [_sz, _sz, _sz, _u64p, _u64p]
         L.orc_gemm_points_f64.argtypes = [_sz, _u64p, _u64p, _sz, _f32p, _sz, _f32p, _sz,
                                           _f32p, _sz, ctypes.c_double, ctypes.c_double,
@@ -128,6 +129,14 @@ def saxpy(alpha, x, y):
     x, y = _c32(x), _c32(y)
     out = np.empty_like(x)
     lib().orc_saxpy(x.size, alpha, _p(x, _f32p), _p(y, _f32p), _p(out, _f32p))
+    return out
+
+
+def saxpy_mt(alpha, x, y):
+    """saxpy over the host cores (OpenMP); the same bits as saxpy()."""
+    x, y = _c32(x), _c32(y)
+    out = np.empty_like(x)
+    lib().orc_saxpy_mt(x.size, alpha, _p(x, _f32p), _p(y, _f32p), _p(out, _f32p))
     return out
 
 

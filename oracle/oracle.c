@@ -155,6 +155,16 @@ void orc_saxpy(size_t n, float alpha, const float *x, const float *y, float *out
     }
 }
 
+/* The same, split over the host cores (OpenMP): the timed CPU baseline of
+ * the saxpy config. */
+void orc_saxpy_mt(size_t n, float alpha, const float *x, const float *y, float *out) {
+#pragma omp parallel for schedule(static)
+    for (long i = 0; i < (long)n; ++i) {
+        volatile float p = alpha * x[i];
+        out[i] = p + y[i];
+    }
+}
+
 /* --------------------------------------------------------------- gemm */
 /* xorshift64 point sampler of main.rs:399-410: (0,0), (M-1,N-1), then
  * (sample(M), sample(N)) with sample(l) = state % l after each step. */

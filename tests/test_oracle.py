@@ -268,3 +268,11 @@ def test_sgemm_baseline_agrees():
     got = oracle.sgemm_f32(0.125, A, B, 1.5, C)
     want = oracle.gemm_full(A, B, C, 0.125, 1.5)
     assert np.allclose(got, want, rtol=1e-5, atol=1e-5)
+
+
+def test_saxpy_mt_matches_scalar_saxpy():
+    # the multi-core CPU baseline computes the same bits as the scalar oracle
+    n = 1_000_003
+    x, y = oracle.lcg_f32(11, n), oracle.lcg_f32(12, n)
+    a = oracle.saxpy_mt(np.float32(2.5), x, y)
+    assert np.array_equal(a.view(np.uint32), oracle.saxpy(np.float32(2.5), x, y).view(np.uint32))
