@@ -112,7 +112,15 @@ int phx_kernel_abi(phx_kernel k, int *index_bits, uint32_t block[3]);
 
 /* ------------------------------------------------------------ launch */
 /* cuLaunchKernel semantics: one pointer per kernel parameter in args
- * (stream.launch, engine.rs:643-647; launch!, main.rs:308-323). */
+ * (stream.launch, engine.rs:643-647; launch!, main.rs:308-323).
+ * For a built-in kernel (phx_builtin_function, or phx_module_get_function on
+ * a phx_module_load_file of a built-in code object) the runtime reads the
+ * extents from the argument list, checks them as the kernel would, and
+ * replaces grid, block and shared_bytes with its own (the reference caller's
+ * saxpy 1024-thread blocks and flash @launch(128) are accepted).  A built-in
+ * GEMM or flash launch whose problem cannot fill the GPU runs split over K
+ * or over the keys (phx_split_plan), with a workspace taken from HIP's
+ * stream-ordered memory pool and released on s. */
 int phx_launch(phx_function f, const uint32_t grid[3], const uint32_t block[3],
                uint32_t shared_bytes, phx_stream s, void **args);
 
@@ -138,6 +146,13 @@ int phx_launch_by_name(const char *ph_file, const char *entry, const uint32_t gr
                        const uint32_t block[3], phx_stream s, void **args);
 /* Validates that a built-in kernel accepts these dims (divisibility etc). */
 int phx_check_shape(phx_kernel k, const int64_t *dims, int ndims);
+/* The split a launch of k over dims (as phx_grid_for) runs with: *splits K
+ * chunks (gemm_fp32, gemm_fp16tc_fp32acc, gemm_fp16) or key chunks (flash),
+ * 1 for none, and the workspace bytes that needs (0 for none).  Other
+ * kernels never split.  No counterpart in the reference, whose autotuner
+ * picks tile sizes instead (phobos-bench/src/autotune.rs:98-192). */
+int phx_split_plan(phx_kernel k, const int64_t *dims, int ndims, int *splits,
+                   size_t *workspace_bytes);
 
 /* --- Pod COMPUTE marshalling (engine.rs:582-630) ---
  * Each tile argument becomes the exploded memref

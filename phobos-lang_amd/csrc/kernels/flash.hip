@@ -431,10 +431,15 @@ __device__ __forceinline__ void flash16_last(Flash16 &fs, const char *cur, uint3
     pv(fs.acc, cur + KV_TILE, pf, lane);
 }
 
+// One block of queries q0 .. q0 + 255 over keys 0 .. Nk-1.  PART: instead of
+// O, store each query's unnormalised accumulator (64 f32 at pacc + 64 q) and
+// its running max (log2 units) and row sum (pml + 2 q), for flash_combine.
+template <bool PART>
 __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp, T *O,
                                             int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo,
                                             uint32_t Nq, uint32_t Nk, uint32_t q0, float scale,
-                                            char *st0, char *st1, char *st2, char *st3) {
+                                            char *st0, char *st1, char *st2, char *st3,
+                                            float *pacc, float *pml) {
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t lq = lane & 31, g = lane >> 5;
@@ -502,7 +507,17 @@ __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp
     // acc[dt][r]: d = 32dt + 8(r/4) + 4g + r%4, query qw + lq.
     fs.l = xor32_add(fs.l);  // both halves of the query's row sum
     const uint32_t q = qw + lq;
-    if (q < Nq) {
+    if (PART && q < Nq) {
+        float *arow = pacc + (int64_t)q * D;
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+                *(phx_f4 *)(arow + 32 * dt + 8 * b + 4 * g) =
+                    (phx_f4){fs.acc[dt][4 * b], fs.acc[dt][4 * b + 1], fs.acc[dt][4 * b + 2],
+                             fs.acc[dt][4 * b + 3]};
+        if (g == 0) *(float2 *)(pml + 2 * (int64_t)q) = make_float2(fs.m2, fs.l);
+    } else if (q < Nq) {
         T *orow = O + (int64_t)q * ldo;
 #pragma unroll
         for (int dt = 0; dt < 2; ++dt)
@@ -582,10 +597,13 @@ __device__ __forceinline__ void store_v(const Stage &st, char *Vt, uint32_t tid)
 
 #define RESCALE_SLACK 8.0f
 
+// One block of queries q0 .. q0 + 127 over keys 0 .. Nk-1; PART as in the
+// f16 path.
+template <bool PART>
 __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp, T *O,
                                             int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo,
                                             uint32_t Nq, uint32_t Nk, uint32_t q0, float scale,
-                                            char (*lds)[2][TILE_BYTES]) {
+                                            char (*lds)[2][TILE_BYTES], float *pacc, float *pml) {
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t lq = lane & 31, g = lane >> 5;
     const uint32_t myq = q0 + wave * 32 + lq;
@@ -695,6 +713,18 @@ __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp
     }
 
     if (myq >= Nq) return;
+    if (PART) {
+        float *arow = pacc + (int64_t)myq * D;
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+                *(phx_f4 *)(arow + 32 * dt + 8 * b + 4 * g) =
+                    (phx_f4){acc[dt][4 * b], acc[dt][4 * b + 1], acc[dt][4 * b + 2],
+                             acc[dt][4 * b + 3]};
+        if (g == 0) *(float2 *)(pml + 2 * (int64_t)myq) = make_float2(m2, l);
+        return;
+    }
     T *orow = O + (int64_t)myq * ldo;
 #pragma unroll
     for (int dt = 0; dt < 2; ++dt)
@@ -713,12 +743,18 @@ __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp
 // one array, so every stage address is a constant offset from one base
 #define FA_LDS_DECL __shared__ __attribute__((aligned(16))) char st[NSTAGE][STAGE_BYTES];
 #define FA_CALL(Qp, Kp, Vp, Op, ldq, ldk, ldv, ldo, Nq, Nk, q0) \
-    flash_block(Qp, Kp, Vp, Op, ldq, ldk, ldv, ldo, Nq, Nk, q0, scale, st[0], st[1], st[2], st[3])
+    flash_block<false>(Qp, Kp, Vp, Op, ldq, ldk, ldv, ldo, Nq, Nk, q0, scale, st[0], st[1], \
+                       st[2], st[3], nullptr, nullptr)
+#define FA_CALL_PART(Qp, Kp, Vp, ldq, ldk, ldv, Nq, Nk, q0, pacc, pml)                    \
+    flash_block<true>(Qp, Kp, Vp, nullptr, ldq, ldk, ldv, 0, Nq, Nk, q0, scale, st[0], st[1], \
+                      st[2], st[3], pacc, pml)
 #else
 #define FA_QB BR
 #define FA_LDS_DECL __shared__ __attribute__((aligned(16))) char lds[2][2][TILE_BYTES];
 #define FA_CALL(Qp, Kp, Vp, Op, ldq, ldk, ldv, ldo, Nq, Nk, q0) \
-    flash_block(Qp, Kp, Vp, Op, ldq, ldk, ldv, ldo, Nq, Nk, q0, scale, lds)
+    flash_block<false>(Qp, Kp, Vp, Op, ldq, ldk, ldv, ldo, Nq, Nk, q0, scale, lds, nullptr, nullptr)
+#define FA_CALL_PART(Qp, Kp, Vp, ldq, ldk, ldv, Nq, Nk, q0, pacc, pml) \
+    flash_block<true>(Qp, Kp, Vp, nullptr, ldq, ldk, ldv, 0, Nq, Nk, q0, scale, lds, pacc, pml)
 #endif
 
 extern "C" __global__ __launch_bounds__(NT, FA_WAVES_PER_SIMD) void flash_attention(PHX_MEMREF2(T, q, int64_t),
@@ -761,5 +797,64 @@ extern "C" __global__ __launch_bounds__(NT, FA_WAVES_PER_SIMD) void flash_attent
         FA_CALL(q_ptr + q_off + h * q_st0, k_ptr + k_off + h * k_st0, v_ptr + v_off + h * v_st0,
                 o_ptr + o_off + h * o_st0, q_st1, k_st1, v_st1, o_st1, (uint32_t)Nq, (uint32_t)Nk,
                 rb * FA_QB);
+    }
+}
+
+// Split keys, for launches with too few query blocks to fill the GPU (the
+// host picks the split; see phx_runtime.cpp).  Workgroup (x, y) runs query
+// block x % nrb of head x / nrb over keys [y * kchunk, min(Nk, (y+1) * kchunk))
+// and stores each query's unnormalised accumulator, running max and row sum
+// into the workspace W, laid out for splits s, heads h, queries q as
+//   acc: W[((s * BH + h) * Nq + q) * 64 + d]
+//   m, l: W[nsplit * BH * Nq * 64 + ((s * BH + h) * Nq + q) * 2 + {0, 1}].
+// Each chunk is the same online softmax over its own keys (kchunk is a
+// multiple of the 64-key block), so flash_combine only has to merge them.
+// Head strides hq, hk, hv are in elements (0 for one head).
+extern "C" __global__ __launch_bounds__(NT, FA_WAVES_PER_SIMD) void flash_attention_split(
+    const T *Qb, const T *Kb, const T *Vb, float *W, int64_t BH, int64_t Nq, int64_t Nk,
+    int64_t ldq, int64_t ldk, int64_t ldv, int64_t hq, int64_t hk, int64_t hv, int64_t kchunk,
+    int32_t nsplit, float scale) {
+    FA_LDS_DECL
+    const uint32_t nrb = (uint32_t)((Nq + FA_QB - 1) / FA_QB);
+    const int64_t k0 = (int64_t)blockIdx.y * kchunk;
+    if (blockDim.x != NT || blockIdx.x >= nrb * (uint32_t)BH || k0 >= Nk || kchunk % BC) return;
+    const uint32_t h = blockIdx.x / nrb, rb = blockIdx.x % nrb;
+    const int64_t nk = Nk - k0 < kchunk ? Nk - k0 : kchunk;
+    const int64_t plane = ((int64_t)blockIdx.y * BH + h) * Nq;
+    float *pacc = W + plane * D;
+    float *pml = W + (int64_t)nsplit * BH * Nq * D + plane * 2;
+    FA_CALL_PART(Qb + h * hq, Kb + h * hk + k0 * ldk, Vb + h * hv + k0 * ldv, ldq, ldk, ldv,
+                 (uint32_t)Nq, (uint32_t)nk, rb * FA_QB, pacc, pml);
+}
+
+// Merges the nsplit partial results of flash_attention_split: per query,
+// M = max_s m_s, w_s = 2^(m_s - M), O = (sum_s w_s acc_s) / (sum_s w_s l_s),
+// rounded once to T.  Four d of one query per thread; head stride ho and row
+// stride ldo of O in elements.
+extern "C" __global__ __launch_bounds__(256) void flash_combine(const float *W, int32_t nsplit,
+                                                                T *O, int64_t BH, int64_t Nq,
+                                                                int64_t ldo, int64_t ho) {
+    const int64_t nq = BH * Nq, total = nq * (D / 4);
+    const float *ml = W + (int64_t)nsplit * nq * D;
+    for (int64_t i = (int64_t)phx_block_linear() * blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)phx_block_count() * blockDim.x) {
+        const int64_t hqi = i / (D / 4), d4 = i % (D / 4);
+        float mx = ml[2 * hqi];
+        for (int32_t s = 1; s < nsplit; ++s) mx = fmaxf(mx, ml[2 * (s * nq + hqi)]);
+        float l = 0.0f;
+        phx_f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int32_t s = 0; s < nsplit; ++s) {
+            const float w = __builtin_amdgcn_exp2f(ml[2 * (s * nq + hqi)] - mx);
+            l = l + w * ml[2 * (s * nq + hqi) + 1];
+            acc = acc + w * *(const phx_f4 *)(W + (s * nq + hqi) * D + 4 * d4);
+        }
+        const int64_t h = hqi / Nq, q = hqi % Nq;
+        T *dst = O + h * ho + q * ldo + 4 * d4;
+#ifdef PHX_FLASH_F16
+        *(phx_h4 *)dst = (phx_h4){(_Float16)(acc[0] / l), (_Float16)(acc[1] / l),
+                                  (_Float16)(acc[2] / l), (_Float16)(acc[3] / l)};
+#else
+        *(phx_f4 *)dst = acc / l;
+#endif
     }
 }

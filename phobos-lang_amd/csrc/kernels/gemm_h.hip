@@ -161,8 +161,8 @@ __device__ __forceinline__ void mfma_all(phx_f16v (&acc)[4][4], const Frags &f) 
 // for the tile.  No per-store test: an explicit bounds check on every store
 // cost gemm_fp16 5% through its branches and exec-mask updates.  R (ragged)
 // false: the tile lies inside C and stores go through plain pointers.
-template <bool R>
-__device__ __forceinline__ void epilogue(const phx_f16v (&acc)[4][4], float *ep_all, TOut *C,
+template <bool R, typename TO>
+__device__ __forceinline__ void epilogue(const phx_f16v (&acc)[4][4], float *ep_all, TO *C,
                                          int64_t ldc, int64_t M, int64_t N, uint32_t m0,
                                          uint32_t n0, uint32_t wm, uint32_t wn, float alpha,
                                          float beta, uint32_t wave, uint32_t lane) {
@@ -171,15 +171,15 @@ __device__ __forceinline__ void epilogue(const phx_f16v (&acc)[4][4], float *ep_
     const uint32_t ml = (uint32_t)M - m0;
     const uint32_t rows = ml < BM ? ml : BM;  // rows of the tile that exist
     const __amdgpu_buffer_rsrc_t rc =
-        phx_rsrc(C + (int64_t)m0 * ldc, rows * (uint32_t)ldc * (uint32_t)sizeof(TOut));
+        phx_rsrc(C + (int64_t)m0 * ldc, rows * (uint32_t)ldc * (uint32_t)sizeof(TO));
     // lane part of the offset (row wm + lane/32, its 4 columns); a store adds
     // the uniform row step in the scalar offset.  The empty asm keeps the
     // compiler from hoisting per-store offsets out of the tile loop, where
     // they would stay live (and spill) across the K loop.
-    const uint32_t pitch = (uint32_t)ldc * (uint32_t)sizeof(TOut);
+    const uint32_t pitch = (uint32_t)ldc * (uint32_t)sizeof(TO);
     const uint32_t col = n0 + wn + (lane & 31) * 4;
     uint32_t voff = (wm + (lane >> 5)) * pitch +
-                    (col < (uint32_t)N ? col * (uint32_t)sizeof(TOut) : 0x80000000u);
+                    (col < (uint32_t)N ? col * (uint32_t)sizeof(TO) : 0x80000000u);
     asm volatile("" : "+v"(voff));
 #pragma unroll
     for (int pass = 0; pass < WM / EP_RP; ++pass) {
@@ -201,8 +201,8 @@ __device__ __forceinline__ void epilogue(const phx_f16v (&acc)[4][4], float *ep_
             // row of the tile * pitch + column: < 2^31 in range (the host
             // limits 257 rows of C to 2 GiB); + 2^31 when the column is past N
             const int so = (int)((pass * EP_RP + rr * 2) * pitch);
-            TOut *dst = C + (int64_t)(m0 + wm + pass * EP_RP + row) * ldc + n0 + wn + c4;
-#ifdef PHX_GEMM_TC
+            TO *dst = C + (int64_t)(m0 + wm + pass * EP_RP + row) * ldc + n0 + wn + c4;
+            if constexpr (sizeof(TO) == 4) {  // f32 output
             phx_f4 o = v;
             if (beta != 0.0f) {
                 const phx_f4 c = R ? __builtin_bit_cast(phx_f4, __builtin_amdgcn_raw_buffer_load_b128(
@@ -214,7 +214,7 @@ __device__ __forceinline__ void epilogue(const phx_f16v (&acc)[4][4], float *ep_
                 __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(phx_u4, o), rc, (int)voff, so, 0);
             else
                 *(phx_f4 *)dst = o;
-#else
+            } else {  // f16 output
             float o[4] = {v.x, v.y, v.z, v.w};
             if (beta != 0.0f) {
                 const phx_h4 c = R ? __builtin_bit_cast(phx_h4, __builtin_amdgcn_raw_buffer_load_b64(
@@ -233,7 +233,7 @@ __device__ __forceinline__ void epilogue(const phx_f16v (&acc)[4][4], float *ep_
                 __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(phx_u2, h), rc, (int)voff, so, 0);
             else
                 *(phx_h4 *)dst = h;
-#endif
+            }
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -516,10 +516,13 @@ __device__ __forceinline__ void dma4_k_step(phx_f16v (&acc)[4][4], Frags &F0, Fr
 // step read zero and C is stored through a bounded resource; whole-tile
 // shapes run the instance without any of that (the masks cost gemm_fp16tc
 // 2% when always on).
-template <bool RG>
-__device__ __forceinline__ void gemm_body(const TIn *A, const TIn *B, TOut *C, int64_t lda,
+// Tiles t0, t0 + tstride, ... of C (the regular entry walks them with the
+// linear block id over the whole grid; the split-K entry with blockIdx.x).
+template <bool RG, typename TO>
+__device__ __forceinline__ void gemm_body(const TIn *A, const TIn *B, TO *C, int64_t lda,
                                           int64_t ldb, int64_t ldc, int64_t M, int64_t N,
-                                          int64_t K, float alpha, float beta,
+                                          int64_t K, float alpha, float beta, uint32_t t0,
+                                          uint32_t tstride,
 #ifdef PHX_GEMM_TC
                                           char *stg
 #else
@@ -540,7 +543,7 @@ __device__ __forceinline__ void gemm_body(const TIn *A, const TIn *B, TOut *C, i
     const uint32_t tiles_n = (uint32_t)((N + BN - 1) / BN);
     const uint32_t tiles_m = (uint32_t)((M + BM - 1) / BM);
     const uint32_t ntiles = tiles_m * tiles_n;
-    const uint32_t nblk = phx_block_count();
+    const uint32_t nblk = tstride;
     const uint32_t nk = (uint32_t)((K + BK - 1) / BK);
 #ifdef PHX_GEMM_TC
     const uint32_t voa = (uint32_t)(((tid >> 2) * lda + (tid & 3) * 8) * ESZ);
@@ -557,7 +560,7 @@ __device__ __forceinline__ void gemm_body(const TIn *A, const TIn *B, TOut *C, i
         (uint32_t)(((lane >> 5) * ldb + 8 * ((lane & 31) ^ (4 * (2 + (lane >> 5))))) * 2);
 #endif
 
-    for (uint32_t t = phx_block_linear(); t < ntiles; t += nblk) {
+    for (uint32_t t = t0; t < ntiles; t += nblk) {
         const uint32_t ts = nblk == ntiles ? phx_xcd_swizzle(t, ntiles) : t;
         const uint32_t gsz = GROUP_M * tiles_n;
         const uint32_t g0 = (ts / gsz) * GROUP_M;
@@ -607,7 +610,7 @@ __device__ __forceinline__ void gemm_body(const TIn *A, const TIn *B, TOut *C, i
 #undef TC3
         PHX_WAIT_VMCNT(0);
         __syncthreads();
-        epilogue<RG>(acc, (float *)stg0, C, ldc, M, N, m0, n0, wm, wn, alpha, beta, wave, lane);
+        epilogue<RG, TO>(acc, (float *)stg0, C, ldc, M, N, m0, n0, wm, wn, alpha, beta, wave, lane);
         __syncthreads();
 #else
 #pragma unroll
@@ -630,7 +633,7 @@ __device__ __forceinline__ void gemm_body(const TIn *A, const TIn *B, TOut *C, i
                             N, K, m0, n0, kt + u, voa, voa_t, vob0, vob1, wm, wn, wave, lane);
         PHX_WAIT_VMCNT(0);
         __syncthreads();
-        epilogue<RG>(acc, (float *)stg0, C, ldc, M, N, m0, n0, wm, wn, alpha, beta, wave, lane);
+        epilogue<RG, TO>(acc, (float *)stg0, C, ldc, M, N, m0, n0, wm, wn, alpha, beta, wave, lane);
         __syncthreads();
 #endif
     }
@@ -673,8 +676,52 @@ extern "C" __global__ __launch_bounds__(NT, 1) void gemm(PHX_MEMREF2(TIn, a, int
 #define GEMM_LDS stg0, stg1, stg2, stg3
 #endif
     if (M % BM == 0 && N % BN == 0 && K % BK == 0)  // uniform
-        gemm_body<false>(A, B, C, lda, ldb, ldc, M, N, K, alpha, beta, GEMM_LDS);
+        gemm_body<false, TOut>(A, B, C, lda, ldb, ldc, M, N, K, alpha, beta, phx_block_linear(),
+                               phx_block_count(), GEMM_LDS);
     else
-        gemm_body<true>(A, B, C, lda, ldb, ldc, M, N, K, alpha, beta, GEMM_LDS);
+        gemm_body<true, TOut>(A, B, C, lda, ldb, ldc, M, N, K, alpha, beta, phx_block_linear(),
+                              phx_block_count(), GEMM_LDS);
+}
+
+// Split-K for shapes with too few output tiles to fill the GPU (the host
+// picks the split; see phx_runtime.cpp).  Workgroup (x, y) computes tiles
+// x, x + gridDim.x, ... over the K columns [y * kchunk, min(K, (y+1) * kchunk))
+// and stores the raw f32 sums to W + y * M * N (row-major, row pitch N):
+// the tile kernel run on the sub-matrices A[:, k0:k1] and B[k0:k1, :] with
+// alpha 1 and beta 0, so C is not read.  kchunk is a multiple of BK, so each
+// chunk starts 16-byte aligned; a chunk's partial last step is masked as the
+// last step of any K is.  gemm_splitk_reduce then applies the epilogue.
+extern "C" __global__ __launch_bounds__(NT, 1) void gemm_splitk(const TIn *A, const TIn *B,
+                                                                 float *W, int64_t lda,
+                                                                 int64_t ldb, int64_t M,
+                                                                 int64_t N, int64_t K,
+                                                                 int64_t kchunk) {
+#ifdef PHX_GEMM_TC
+    __shared__ __attribute__((aligned(16))) char stg[3 * STAGE_BYTES];
+#else
+    __shared__ __attribute__((aligned(16))) char stg0[STAGE_BYTES];
+    __shared__ __attribute__((aligned(16))) char stg1[STAGE_BYTES];
+    __shared__ __attribute__((aligned(16))) char stg2[STAGE_BYTES];
+    __shared__ __attribute__((aligned(16))) char stg3[STAGE_BYTES];
+#endif
+    const int64_t k0 = (int64_t)blockIdx.y * kchunk;
+    if (blockDim.x != NT || k0 >= K || kchunk % BK) return;
+    const int64_t kc = K - k0 < kchunk ? K - k0 : kchunk;
+    const TIn *As = A + k0;
+    const TIn *Bs = B + k0 * ldb;
+    float *Ws = W + (int64_t)blockIdx.y * M * N;
+    if (M % BM == 0 && N % BN == 0 && kc % BK == 0)
+        gemm_body<false, float>(As, Bs, Ws, lda, ldb, N, M, N, kc, 1.0f, 0.0f, blockIdx.x,
+                                gridDim.x, GEMM_LDS);
+    else
+        gemm_body<true, float>(As, Bs, Ws, lda, ldb, N, M, N, kc, 1.0f, 0.0f, blockIdx.x,
+                               gridDim.x, GEMM_LDS);
+}
 #undef GEMM_LDS
+
+extern "C" __global__ __launch_bounds__(256) void gemm_splitk_reduce(const float *W, int32_t S,
+                                                                      TOut *C, int64_t ldc,
+                                                                      int64_t M, int64_t N,
+                                                                      float alpha, float beta) {
+    phx_splitk_reduce(W, S, C, ldc, M, N, alpha, beta);
 }

@@ -49,7 +49,7 @@
 
 #define BM PHX_S_TILE
 #define BN PHX_S_TILE
-#define BK 16
+#define BK PHX_S_BK
 #define NT PHX_S_THREADS
 #define WM 128
 #define WN 128
@@ -236,11 +236,14 @@ __device__ __forceinline__ void epilogue(const phx_f16v (&acc)[4][4], float *ep_
     }
 }
 
+// Tiles t0, t0 + tstride, ... of C (the regular entries walk them with the
+// linear block id over the whole grid; the split-K entry with blockIdx.x).
 template <bool STEP>
 __device__ __forceinline__ void gemm_s_body(const float *A, int64_t lda, const float *B,
                                             int64_t ldb, float *C, int64_t ldc, int64_t M,
                                             int64_t N, int64_t K, float alpha, float beta,
-                                            char *stg0, char *stg1, char *stg2) {
+                                            char *stg0, char *stg1, char *stg2, uint32_t t0,
+                                            uint32_t tstride) {
     char *const S[NSTG] = {stg0, stg1, stg2};
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63;
@@ -250,7 +253,7 @@ __device__ __forceinline__ void gemm_s_body(const float *A, int64_t lda, const f
     const uint32_t tiles_n = (uint32_t)((N + BN - 1) / BN);
     const uint32_t tiles_m = (uint32_t)((M + BM - 1) / BM);
     const uint32_t ntiles = tiles_m * tiles_n;
-    const uint32_t nblk = phx_block_count();
+    const uint32_t nblk = tstride;
     const uint32_t nk = (uint32_t)((K + BK - 1) / BK);
     const uint32_t voa =
         (uint32_t)(((lane >> 2) * lda + 4 * ((lane & 3) ^ ((lane >> 4) & 3))) * 4);
@@ -262,7 +265,7 @@ __device__ __forceinline__ void gemm_s_body(const float *A, int64_t lda, const f
     const uint32_t vob0 = lane * 16;
     const uint32_t vob1 = (lane ^ 8) * 16;
 
-    for (uint32_t t = phx_block_linear(); t < ntiles; t += nblk) {
+    for (uint32_t t = t0; t < ntiles; t += nblk) {
         const uint32_t ts = nblk == ntiles ? phx_xcd_swizzle(t, ntiles) : t;
         const uint32_t gsz = GROUP_M * tiles_n;
         const uint32_t g0 = (ts / gsz) * GROUP_M;
@@ -321,7 +324,35 @@ extern "C" __global__ __launch_bounds__(NT, 1) void gemm(PHX_MEMREF2(float, a, i
                                                           float alpha, float beta) {
     GEMM_S_PRELUDE
     gemm_s_body<false>(a_ptr + a_off, a_st0, b_ptr + b_off, b_st0, c_ptr + c_off, c_st0, M, N, K,
-                       alpha, beta, stg0, stg1, stg2);
+                       alpha, beta, stg0, stg1, stg2, phx_block_linear(), phx_block_count());
+}
+
+// Split-K for shapes with too few output tiles to fill the GPU (the host
+// picks the split; see phx_runtime.cpp).  Workgroup (x, y) computes tiles
+// x, x + gridDim.x, ... over the K columns [y * kchunk, min(K, (y+1) * kchunk))
+// and stores the raw f32 sums to W + y * M * N (row-major, row pitch N): the
+// tile kernel on the sub-matrices A[:, k0:k1] and B[k0:k1, :] with alpha 1
+// and beta 0.  gemm_splitk_reduce then applies the epilogue.
+extern "C" __global__ __launch_bounds__(NT, 1) void gemm_splitk(const float *A, const float *B,
+                                                                 float *W, int64_t lda,
+                                                                 int64_t ldb, int64_t M,
+                                                                 int64_t N, int64_t K,
+                                                                 int64_t kchunk) {
+    __shared__ __attribute__((aligned(16))) char stg0[STAGE_BYTES];
+    __shared__ __attribute__((aligned(16))) char stg1[STAGE_BYTES];
+    __shared__ __attribute__((aligned(16))) char stg2[STAGE_BYTES];
+    const int64_t k0 = (int64_t)blockIdx.y * kchunk;
+    if (blockDim.x != NT || k0 >= K || kchunk % BK) return;
+    const int64_t kc = K - k0 < kchunk ? K - k0 : kchunk;
+    gemm_s_body<false>(A + k0, lda, B + k0 * ldb, ldb, W + (int64_t)blockIdx.y * M * N, N, M, N,
+                       kc, 1.0f, 0.0f, stg0, stg1, stg2, blockIdx.x, gridDim.x);
+}
+
+extern "C" __global__ __launch_bounds__(256) void gemm_splitk_reduce(const float *W, int32_t S,
+                                                                      float *C, int64_t ldc,
+                                                                      int64_t M, int64_t N,
+                                                                      float alpha, float beta) {
+    phx_splitk_reduce(W, S, C, ldc, M, N, alpha, beta);
 }
 #endif
 
@@ -332,7 +363,7 @@ extern "C" __global__ __launch_bounds__(NT, 1) void matmul(PHX_MEMREF2(float, a,
                                                             float alpha, float beta) {
     GEMM_S_PRELUDE
     gemm_s_body<true>(a_ptr + a_off, a_st0, b_ptr + b_off, b_st0, c_ptr + c_off, c_st0, M, N, K,
-                      alpha, beta, stg0, stg1, stg2);
+                      alpha, beta, stg0, stg1, stg2, phx_block_linear(), phx_block_count());
 }
 
 // C = fl(beta * C) over a [M, N] tile: an HBM stream of 8 bytes per element.

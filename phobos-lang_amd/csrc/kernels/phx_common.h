@@ -50,3 +50,36 @@ __device__ __forceinline__ uint32_t phx_pack_h2(float lo, float hi) {
     v.y = (_Float16)hi;
     return __builtin_bit_cast(uint32_t, v);
 }
+
+// The split-K epilogue shared by the GEMM code objects: acc = W[0] + W[1] +
+// ... + W[S-1] over S partial-sum planes of M x N f32 (in that order, so the
+// result does not depend on timing), then C = fl(fl(alpha*acc) +
+// fl(beta*c_old)) with C not read when beta == 0, rounded once to the output
+// type.  Four consecutive elements per thread (N is a multiple of 4, C's
+// rows are 16-byte (f32) or 8-byte (f16) aligned), block-stride over the
+// M x N/4 groups.  Compiled -ffp-contract=off: every mul and add rounds.
+template <typename TO>
+__device__ __forceinline__ void phx_splitk_reduce(const float *W, int32_t S, TO *C, int64_t ldc,
+                                                  int64_t M, int64_t N, float alpha, float beta) {
+    const int64_t ng = M * (N / 4), plane = M * N;
+    for (int64_t gi = (int64_t)phx_block_linear() * blockDim.x + threadIdx.x; gi < ng;
+         gi += (int64_t)phx_block_count() * blockDim.x) {
+        const int64_t e = gi * 4;
+        const int64_t r = e / N, c = e % N;
+        phx_f4 acc = *(const phx_f4 *)(W + e);
+        for (int32_t sp = 1; sp < S; ++sp) acc = acc + *(const phx_f4 *)(W + sp * plane + e);
+        TO *dst = C + r * ldc + c;
+        phx_f4 o = alpha * acc;
+        if constexpr (sizeof(TO) == 4) {
+            if (beta != 0.0f) o = o + beta * *(const phx_f4 *)dst;
+            *(phx_f4 *)dst = o;
+        } else {
+            if (beta != 0.0f) {
+                const phx_h4 h = *(const phx_h4 *)dst;
+                o = o + beta * (phx_f4){(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+            }
+            *(phx_h4 *)dst =
+                (phx_h4){(_Float16)o[0], (_Float16)o[1], (_Float16)o[2], (_Float16)o[3]};
+        }
+    }
+}

@@ -33,8 +33,34 @@
 // f32 GEMM (gemm_fp32, cluster matmul): a workgroup computes a
 // PHX_S_TILE x PHX_S_TILE output tile (4 waves of 128x128).
 #define PHX_S_TILE 256
+#define PHX_S_BK 16
 #define PHX_S_THREADS 256
 #define PHX_S_NK_MULT 4
+
+// Split-K (gemm_fp32, gemm_fp16tc_fp32acc, gemm_fp16): when a GEMM has
+// fewer than PHX_SPLIT_MIN_TILES output tiles, its K range is cut into
+// chunks of whole 32-deep steps computed by separate workgroups
+// (gemm_splitk), whose f32 partial sums gemm_splitk_reduce adds in a fixed
+// order.  At most PHX_SPLIT_MAX chunks, each of at least
+// PHX_SPLIT_MIN_STEPS_F32 (gemm_fp32) or PHX_SPLIT_MIN_STEPS_F16 (the f16
+// MFMA GEMMs, whose K steps are 8x cheaper) 32-deep steps: measured on
+// MI355X at 512^3 .. 2048^3 and 256^2 x 16384, shorter f16 chunks lose more
+// to the partial-sum traffic than they gain.
+#define PHX_SPLIT_MIN_TILES 128
+#define PHX_SPLIT_MAX 16
+#define PHX_SPLIT_MIN_STEPS_F32 1
+#define PHX_SPLIT_MIN_STEPS_F16 32
+#define PHX_SPLIT_KSTEP 32
+#define PHX_REDUCE_THREADS 256
+
+// Split keys (flash attention): when the (query block, head) work items
+// cannot fill half of the PHX_FA_SLOTS workgroup slots (256 CUs x 2
+// resident workgroups), the keys are cut into chunks of whole 64-key blocks,
+// at least PHX_FLASH_SPLIT_MIN_BLOCKS each and at most PHX_SPLIT_MAX chunks,
+// run as separate workgroups (flash_attention_split) and merged by
+// flash_combine.
+#define PHX_FA_SLOTS 512
+#define PHX_FLASH_SPLIT_MIN_BLOCKS 8
 
 // matmul_init: element-wise, 256 threads x 4 float4.
 #define PHX_EW_THREADS 256

@@ -70,6 +70,7 @@ struct State {
     // built-in they are; under mu.
     std::unordered_map<hipModule_t, std::string> module_files;  // module -> file name
     std::unordered_map<hipFunction_t, std::pair<int, hipModule_t>> aliases;
+    std::unordered_map<std::string, hipFunction_t> aux;  // "file:entry" -> function
     std::mutex mu;
 };
 static State g;
@@ -132,6 +133,40 @@ int builtin(phx_kernel k, hipFunction_t *out) {
         g.fns[k].store(f, std::memory_order_release);
     }
     *out = g.fns[k].load(std::memory_order_relaxed);
+    return PHX_OK;
+}
+
+// Entry points of the built-in code objects that no .ph kernel names (the
+// split-K and split-key kernels the runtime launches itself), by file and
+// entry name; loaded on first use.
+static int aux_function(const char *file, const char *entry, hipFunction_t *out) {
+    if (int rc = ensure_init()) return rc;
+    std::lock_guard<std::mutex> lock(g.mu);
+    const std::string key = std::string(file) + ":" + entry;
+    auto fit = g.aux.find(key);
+    if (fit != g.aux.end()) {
+        *out = fit->second;
+        return PHX_OK;
+    }
+    hipModule_t mod;
+    auto it = g.modules.find(file);
+    if (it == g.modules.end()) {
+        std::string path = g.dir + "/" + file;
+        hipError_t e = hipModuleLoad(&mod, path.c_str());
+        if (e != hipSuccess)
+            return set_error(PHX_E_NOT_FOUND, "cannot load code object %s: %s (build the backend first)",
+                             path.c_str(), hipGetErrorString(e));
+        g.modules[file] = mod;
+    } else {
+        mod = it->second;
+    }
+    hipFunction_t f;
+    hipError_t e = hipModuleGetFunction(&f, mod, entry);
+    if (e != hipSuccess)
+        return set_error(PHX_E_NOT_FOUND, "entry '%s' not in %s: %s", entry, file,
+                         hipGetErrorString(e));
+    g.aux[key] = f;
+    *out = f;
     return PHX_OK;
 }
 
@@ -217,10 +252,9 @@ static void read_descs(void **args, int n, int rank, int bits, int esz, Desc *d)
 // list the way the kernel reads them, after the same consistency checks the
 // kernel makes on entry (a launch that fails them would return without
 // output, so it is refused here instead).
-static int builtin_dims(phx_kernel k, void **args, int64_t *d, int *nd) {
+static int builtin_dims(phx_kernel k, void **args, int64_t *d, int *nd, Desc *t) {
     if (!args) return set_error(PHX_E_INVALID, "%s: null argument list", kSpecs[k].entry);
     const int bits = kSpecs[k].index_bits;
-    Desc t[4];
     auto bad = [&](const char *why) {
         return set_error(PHX_E_INVALID, "%s (%s): %s", kSpecs[k].entry, kSpecs[k].file, why);
     };
@@ -308,6 +342,159 @@ static int builtin_dims(phx_kernel k, void **args, int64_t *d, int *nd) {
     }
 }
 
+// How many K chunks a GEMM is split into (1: no split).  A GEMM whose
+// 256 x 256 output tiles cannot fill half of the 256 CUs gets enough chunks
+// to give every CU a workgroup, within the chunk-length floor of its kernel
+// and at most PHX_SPLIT_MAX chunks.  PHX_GEMM_SPLIT=<n> in the environment
+// forces n (1 turns the split off), for measurement.
+int gemm_split(phx_kernel k, int64_t M, int64_t N, int64_t K) {
+    const int64_t tiles = ((M + PHX_H_BM - 1) / PHX_H_BM) * ((N + PHX_H_BN - 1) / PHX_H_BN);
+    const int64_t steps = (K + PHX_SPLIT_KSTEP - 1) / PHX_SPLIT_KSTEP;
+    int64_t sp;
+    if (const char *env = getenv("PHX_GEMM_SPLIT")) {
+        sp = atoi(env);
+    } else {
+        if (tiles >= PHX_SPLIT_MIN_TILES) return 1;
+        const int64_t min_steps =
+            k == PHX_GEMM_FP32 ? PHX_SPLIT_MIN_STEPS_F32 : PHX_SPLIT_MIN_STEPS_F16;
+        sp = 256 / tiles;
+        if (sp > steps / min_steps) sp = steps / min_steps;
+        if (sp > PHX_SPLIT_MAX) sp = PHX_SPLIT_MAX;
+    }
+    if (sp > steps) sp = steps;
+    if (sp < 2) return 1;
+    // chunks of whole steps; drop chunks the rounding left empty
+    const int64_t per = (steps + sp - 1) / sp;
+    return (int)((steps + per - 1) / per);
+}
+
+// K columns per chunk of a split into sp chunks (a multiple of 32).
+static int64_t split_chunk(int64_t K, int sp) {
+    const int64_t steps = (K + PHX_SPLIT_KSTEP - 1) / PHX_SPLIT_KSTEP;
+    return ((steps + sp - 1) / sp) * PHX_SPLIT_KSTEP;
+}
+
+// Bytes of f32 partial sums a split GEMM needs.
+size_t gemm_split_bytes(int64_t M, int64_t N, int sp) {
+    return (size_t)sp * (size_t)M * (size_t)N * sizeof(float);
+}
+
+// The split-K launches over a caller-provided workspace of
+// gemm_split_bytes(M, N, sp) bytes: gemm_splitk over (tiles, sp) workgroups,
+// then gemm_splitk_reduce, both on stream s.
+int launch_gemm_split_ws(phx_kernel k, const Desc *t, int64_t M, int64_t N, int64_t K,
+                         float alpha, float beta, int sp, hipStream_t s, uint64_t ws) {
+    const char *file = kSpecs[k].file;
+    hipFunction_t fk, fr;
+    if (int rc = aux_function(file, "gemm_splitk", &fk)) return rc;
+    if (int rc = aux_function(file, "gemm_splitk_reduce", &fr)) return rc;
+    const int64_t tiles = ((M + PHX_H_BM - 1) / PHX_H_BM) * ((N + PHX_H_BN - 1) / PHX_H_BN);
+    uint64_t a = t[0].ptr, b = t[1].ptr, c = t[2].ptr;
+    int64_t lda = t[0].stride[0], ldb = t[1].stride[0], ldc = t[2].stride[0];
+    int64_t kchunk = split_chunk(K, sp);
+    void *ka[] = {&a, &b, &ws, &lda, &ldb, &M, &N, &K, &kchunk};
+    hipError_t e = hipModuleLaunchKernel(fk, (uint32_t)tiles, (uint32_t)sp, 1, PHX_H_THREADS, 1, 1,
+                                         0, s, ka, nullptr);
+    if (e != hipSuccess) return hip_error(e, "hipModuleLaunchKernel(gemm_splitk)");
+    int32_t s32 = sp;
+    void *ra[] = {&ws, &s32, &c, &ldc, &M, &N, &alpha, &beta};
+    const int64_t groups = M * (N / 4);
+    int64_t nb = (groups + PHX_REDUCE_THREADS - 1) / PHX_REDUCE_THREADS;
+    if (nb > 8192) nb = 8192;
+    e = hipModuleLaunchKernel(fr, (uint32_t)nb, 1, 1, PHX_REDUCE_THREADS, 1, 1, 0, s, ra, nullptr);
+    if (e != hipSuccess) return hip_error(e, "hipModuleLaunchKernel(gemm_splitk_reduce)");
+    return PHX_OK;
+}
+
+// The same with a stream-ordered workspace taken from HIP's memory pool and
+// returned on the stream after the reduce, so concurrent launches on other
+// streams never share it.
+int launch_gemm_split(phx_kernel k, const Desc *t, int64_t M, int64_t N, int64_t K, float alpha,
+                      float beta, int sp, hipStream_t s) {
+    void *ws = nullptr;
+    hipError_t e = hipMallocAsync(&ws, gemm_split_bytes(M, N, sp), s);
+    if (e != hipSuccess) return hip_error(e, "hipMallocAsync(split-K workspace)");
+    int rc = launch_gemm_split_ws(k, t, M, N, K, alpha, beta, sp, s, (uint64_t)(uintptr_t)ws);
+    e = hipFreeAsync(ws, s);
+    if (rc) return rc;
+    if (e != hipSuccess) return hip_error(e, "hipFreeAsync(split-K workspace)");
+    return PHX_OK;
+}
+
+// How many key chunks a flash launch is split into (1: no split).
+// PHX_FLASH_SPLIT=<n> in the environment forces n, for measurement.
+static bool flash_f16(phx_kernel k) { return k == PHX_FLASH_FP16 || k == PHX_FLASH_FP16_BH; }
+int flash_split(phx_kernel k, int64_t BH, int64_t Nq, int64_t Nk) {
+    const int64_t qb = flash_f16(k) ? PHX_FA16_BR : PHX_FA_BR;
+    const int64_t items = ((Nq + qb - 1) / qb) * BH;
+    const int64_t nkb = (Nk + PHX_FA_BC - 1) / PHX_FA_BC;
+    int64_t sp;
+    if (const char *env = getenv("PHX_FLASH_SPLIT")) {
+        sp = atoi(env);
+    } else {
+        if (2 * items >= PHX_FA_SLOTS) return 1;
+        sp = PHX_FA_SLOTS / items;
+        if (sp > nkb / PHX_FLASH_SPLIT_MIN_BLOCKS) sp = nkb / PHX_FLASH_SPLIT_MIN_BLOCKS;
+        if (sp > PHX_SPLIT_MAX) sp = PHX_SPLIT_MAX;
+    }
+    if (sp > nkb) sp = nkb;
+    if (sp < 2) return 1;
+    const int64_t per = (nkb + sp - 1) / sp;  // blocks per chunk; no empty chunk
+    return (int)((nkb + per - 1) / per);
+}
+
+// Bytes of partial results a split flash launch needs: per chunk and query,
+// 64 accumulators plus the running max and row sum, all f32.
+size_t flash_split_bytes(int64_t BH, int64_t Nq, int sp) {
+    return (size_t)sp * (size_t)BH * (size_t)Nq * (PHX_FA_D + 2) * sizeof(float);
+}
+
+// The split-key launches over a caller-provided workspace of
+// flash_split_bytes(BH, Nq, sp) bytes.  t: the Q, K, V, O descriptors, rank 2
+// (one head) or rank 3 ([BH, N, D]).
+int launch_flash_split_ws(phx_kernel k, const Desc *t, int rank, int64_t BH, int64_t Nq,
+                          int64_t Nk, float scale, int sp, hipStream_t s, uint64_t ws) {
+    const char *file = kSpecs[k].file;
+    hipFunction_t fs, fc;
+    if (int rc = aux_function(file, "flash_attention_split", &fs)) return rc;
+    if (int rc = aux_function(file, "flash_combine", &fc)) return rc;
+    const int64_t qb = flash_f16(k) ? PHX_FA16_BR : PHX_FA_BR;
+    const int64_t items = ((Nq + qb - 1) / qb) * BH;
+    const int64_t nkb = (Nk + PHX_FA_BC - 1) / PHX_FA_BC;
+    int64_t kchunk = ((nkb + sp - 1) / sp) * PHX_FA_BC;
+    uint64_t q = t[0].ptr, kk = t[1].ptr, v = t[2].ptr;
+    const int r = rank - 2;  // index of the row stride
+    int64_t ldq = t[0].stride[r], ldk = t[1].stride[r], ldv = t[2].stride[r], ldo = t[3].stride[r];
+    int64_t hq = r ? t[0].stride[0] : 0, hk = r ? t[1].stride[0] : 0, hv = r ? t[2].stride[0] : 0;
+    int64_t ho = r ? t[3].stride[0] : 0;
+    int32_t nsplit = sp;
+    void *sa[] = {&q, &kk, &v, &ws, &BH, &Nq, &Nk, &ldq, &ldk, &ldv, &hq, &hk, &hv, &kchunk,
+                  &nsplit, &scale};
+    hipError_t e = hipModuleLaunchKernel(fs, (uint32_t)items, (uint32_t)sp, 1, kSpecs[k].block, 1,
+                                         1, 0, s, sa, nullptr);
+    if (e != hipSuccess) return hip_error(e, "hipModuleLaunchKernel(flash_attention_split)");
+    uint64_t o = t[3].ptr;
+    void *ca[] = {&ws, &nsplit, &o, &BH, &Nq, &ldo, &ho};
+    const int64_t threads = BH * Nq * (PHX_FA_D / 4);
+    int64_t nb = (threads + PHX_REDUCE_THREADS - 1) / PHX_REDUCE_THREADS;
+    if (nb > 8192) nb = 8192;
+    e = hipModuleLaunchKernel(fc, (uint32_t)nb, 1, 1, PHX_REDUCE_THREADS, 1, 1, 0, s, ca, nullptr);
+    if (e != hipSuccess) return hip_error(e, "hipModuleLaunchKernel(flash_combine)");
+    return PHX_OK;
+}
+
+int launch_flash_split(phx_kernel k, const Desc *t, int rank, int64_t BH, int64_t Nq, int64_t Nk,
+                       float scale, int sp, hipStream_t s) {
+    void *ws = nullptr;
+    hipError_t e = hipMallocAsync(&ws, flash_split_bytes(BH, Nq, sp), s);
+    if (e != hipSuccess) return hip_error(e, "hipMallocAsync(split-key workspace)");
+    int rc = launch_flash_split_ws(k, t, rank, BH, Nq, Nk, scale, sp, s, (uint64_t)(uintptr_t)ws);
+    e = hipFreeAsync(ws, s);
+    if (rc) return rc;
+    if (e != hipSuccess) return hip_error(e, "hipFreeAsync(split-key workspace)");
+    return PHX_OK;
+}
+
 int launch_raw(hipFunction_t f, const uint32_t grid[3], const uint32_t block[3], uint32_t shmem,
                hipStream_t s, void **args) {
     // A built-in kernel runs on this backend's own tiling, whatever geometry
@@ -318,7 +505,30 @@ int launch_raw(hipFunction_t f, const uint32_t grid[3], const uint32_t block[3],
     if (int k = builtin_id(f); k >= 0) {
         int64_t d[4];
         int nd = 0;
-        if (int rc = builtin_dims((phx_kernel)k, args, d, &nd)) return rc;
+        Desc t[4];
+        if (int rc = builtin_dims((phx_kernel)k, args, d, &nd, t)) return rc;
+        if (k == PHX_GEMM_FP32 || k == PHX_GEMM_FP16TC_FP32ACC || k == PHX_GEMM_FP16) {
+            if (int rc = check_shape((phx_kernel)k, d, nd)) return rc;
+            const int sp = gemm_split((phx_kernel)k, d[0], d[1], d[2]);
+            if (sp > 1) {
+                float alpha, beta;  // the two f32 scalars after the three memrefs
+                memcpy(&alpha, args[21], 4);
+                memcpy(&beta, args[22], 4);
+                return launch_gemm_split((phx_kernel)k, t, d[0], d[1], d[2], alpha, beta, sp, s);
+            }
+        }
+        if (k == PHX_FLASH_FP16 || k == PHX_FLASH_FP32 || k == PHX_FLASH_FP16_BH ||
+            k == PHX_FLASH_FP32_BH) {
+            if (int rc = check_shape((phx_kernel)k, d, nd)) return rc;
+            const bool bh = nd == 4;
+            const int64_t BH = bh ? d[0] : 1, Nq = d[bh], Nk = d[bh + 1];
+            const int sp = flash_split((phx_kernel)k, BH, Nq, Nk);
+            if (sp > 1) {
+                float scale;  // the f32 scalar after the four memrefs
+                memcpy(&scale, args[bh ? 36 : 28], 4);
+                return launch_flash_split((phx_kernel)k, t, bh ? 3 : 2, BH, Nq, Nk, scale, sp, s);
+            }
+        }
         uint32_t g2[3], b2[3];
         if (int rc = grid_for((phx_kernel)k, d, nd, g2, b2)) return rc;
         hipError_t e = hipModuleLaunchKernel(f, g2[0], g2[1], g2[2], b2[0], b2[1], b2[2], 0, s,
@@ -484,6 +694,7 @@ int phx_shutdown(void) {
     for (auto &kv : g.modules) (void)hipModuleUnload(kv.second);
     g.modules.clear();
     for (auto &f : g.fns) f.store(nullptr, std::memory_order_release);
+    g.aux.clear();
     g.init = false;
     return PHX_OK;
 }
@@ -694,6 +905,25 @@ int phx_grid_for(phx_kernel k, const int64_t *dims, int ndims, uint32_t grid[3],
 }
 int phx_check_shape(phx_kernel k, const int64_t *dims, int ndims) {
     return check_shape(k, dims, ndims);
+}
+int phx_split_plan(phx_kernel k, const int64_t *dims, int ndims, int *splits,
+                   size_t *workspace_bytes) {
+    if (int rc = check_shape(k, dims, ndims)) return rc;
+    int sp = 1;
+    size_t ws = 0;
+    if (k == PHX_GEMM_FP32 || k == PHX_GEMM_FP16TC_FP32ACC || k == PHX_GEMM_FP16) {
+        sp = gemm_split(k, dims[0], dims[1], dims[2]);
+        if (sp > 1) ws = gemm_split_bytes(dims[0], dims[1], sp);
+    } else if (k == PHX_FLASH_FP16 || k == PHX_FLASH_FP32 || k == PHX_FLASH_FP16_BH ||
+               k == PHX_FLASH_FP32_BH) {
+        const bool bh = ndims == 4;
+        const int64_t BH = bh ? dims[0] : 1, Nq = dims[bh], Nk = dims[bh + 1];
+        sp = flash_split(k, BH, Nq, Nk);
+        if (sp > 1) ws = flash_split_bytes(BH, Nq, sp);
+    }
+    if (splits) *splits = sp;
+    if (workspace_bytes) *workspace_bytes = ws;
+    return PHX_OK;
 }
 
 int phx_compute(phx_function f, int bits, const phx_tile_arg *tiles, uint32_t ntiles,

@@ -132,6 +132,8 @@ def lib():
     L.phx_launch.argtypes = [_vp, _u32a3, _u32a3, ctypes.c_uint32, _vp, ctypes.POINTER(_vp)]
     L.phx_grid_for.argtypes = [ctypes.c_int, ctypes.POINTER(_i64), ctypes.c_int, _u32a3, _u32a3]
     L.phx_check_shape.argtypes = [ctypes.c_int, ctypes.POINTER(_i64), ctypes.c_int]
+    L.phx_split_plan.argtypes = [ctypes.c_int, ctypes.POINTER(_i64), ctypes.c_int,
+                                 ctypes.POINTER(ctypes.c_int), ctypes.POINTER(_sz)]
     L.phx_compute.argtypes = [_vp, ctypes.c_int, ctypes.POINTER(TileArg), ctypes.c_uint32,
                               ctypes.POINTER(ScalarArg), ctypes.c_uint32, _u32a3, _u32a3, _vp]
     L.phx_saxpy.argtypes = [_vp, _u64, _u64, _u64, _i64, ctypes.c_float]
@@ -363,6 +365,14 @@ def kernel_by_name(ph_file, entry):
 def check_shape(kernel, dims):
     d = (_i64 * len(dims))(*dims)
     return lib().phx_check_shape(kernel, d, len(dims))
+
+
+def split_plan(kernel, dims):
+    """(splits, workspace bytes) of a launch of kernel over dims (phx_split_plan)."""
+    d = (_i64 * len(dims))(*dims)
+    sp, ws = ctypes.c_int(), _sz()
+    check(lib().phx_split_plan(kernel, d, len(dims), ctypes.byref(sp), ctypes.byref(ws)))
+    return sp.value, ws.value
 
 
 def kernel_abi(kernel):
