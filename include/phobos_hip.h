@@ -217,6 +217,22 @@ int phx_arena_free(phx_arena a, uint64_t addr, size_t cls);
 int phx_arena_can_alloc(phx_arena a, size_t bytes); /* 1 yes, 0 no */
 int phx_arena_stats(phx_arena a, size_t *cap, size_t *bump, uint64_t *base);
 
+/* ------------------------------------------------------------ no allocation */
+/* phx_flash_attention_bh without any device allocation.  No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments, split plan, kernels and results (bit for bit)
+ * as phx_flash_attention_bh; a launch split over the keys keeps its partial
+ * results in a fixed PHX_SCRATCH_BYTES (16 MiB) device array that the library
+ * holds on each initialised GPU until the process ends, instead of a pool
+ * workspace.  A split that needs more scratch (phx_split_plan) returns
+ * PHX_E_INVALID; phx_flash_attention_bh takes any size.  Every call on a GPU
+ * shares that GPU's array: calls that overlap on one GPU (several streams or
+ * threads) race. */
+int phx_flash_attention_bh_noalloc(phx_stream s, phx_kernel k, uint64_t q, uint64_t kk,
+                                   uint64_t v, uint64_t o, int64_t BH, int64_t Nq, int64_t Nk,
+                                   int64_t D, float scale);
+
 /* ------------------------------------------------------------ inputs */
 /* Lcg::unit_f32s (phobos-base/src/rng.rs:9-25) into host memory. */
 int phx_lcg_fill_f32(uint64_t seed, size_t n, float *out);

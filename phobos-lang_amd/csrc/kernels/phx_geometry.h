@@ -60,6 +60,9 @@
 // run as separate workgroups (flash_attention_split) and merged by
 // flash_combine.
 #define PHX_FA_SLOTS 512
+// Device bytes of the fixed scratch array behind the allocation-free flash
+// entry point (phx_flash_attention_bh_noalloc): its split-key workspace.
+#define PHX_SCRATCH_BYTES (16u << 20)
 #define PHX_FLASH_SPLIT_MIN_BLOCKS 8
 
 // matmul_init: element-wise, 256 threads x 4 float4.

@@ -139,7 +139,7 @@ int builtin(phx_kernel k, hipFunction_t *out) {
 // Entry points of the built-in code objects that no .ph kernel names (the
 // split-K and split-key kernels the runtime launches itself), by file and
 // entry name; loaded on first use.
-static int aux_function(const char *file, const char *entry, hipFunction_t *out) {
+int aux_function(const char *file, const char *entry, hipFunction_t *out) {
     if (int rc = ensure_init()) return rc;
     std::lock_guard<std::mutex> lock(g.mu);
     const std::string key = std::string(file) + ":" + entry;
@@ -216,13 +216,6 @@ struct ArgPack {
 };
 
 // ------------------------------------------------------------------ raw launches
-// One exploded-memref descriptor read back out of a void** argument list.
-struct Desc {
-    uint64_t ptr = 0;  // aligned pointer + offset, in bytes
-    int64_t size[3] = {0, 0, 0};
-    int64_t stride[3] = {0, 0, 0};
-};
-
 static int64_t arg_idx(void **args, int i, int bits) {
     if (bits == 32) {
         int32_t v;
@@ -452,12 +445,14 @@ size_t flash_split_bytes(int64_t BH, int64_t Nq, int sp) {
 // The split-key launches over a caller-provided workspace of
 // flash_split_bytes(BH, Nq, sp) bytes.  t: the Q, K, V, O descriptors, rank 2
 // (one head) or rank 3 ([BH, N, D]).
+int flash_split_functions(phx_kernel k, hipFunction_t *fs, hipFunction_t *fc) {
+    if (int rc = aux_function(kSpecs[k].file, "flash_attention_split", fs)) return rc;
+    return aux_function(kSpecs[k].file, "flash_combine", fc);
+}
+
 int launch_flash_split_ws(phx_kernel k, const Desc *t, int rank, int64_t BH, int64_t Nq,
-                          int64_t Nk, float scale, int sp, hipStream_t s, uint64_t ws) {
-    const char *file = kSpecs[k].file;
-    hipFunction_t fs, fc;
-    if (int rc = aux_function(file, "flash_attention_split", &fs)) return rc;
-    if (int rc = aux_function(file, "flash_combine", &fc)) return rc;
+                          int64_t Nk, float scale, int sp, hipStream_t s, uint64_t ws,
+                          hipFunction_t fs, hipFunction_t fc) {
     const int64_t qb = flash_f16(k) ? PHX_FA16_BR : PHX_FA_BR;
     const int64_t items = ((Nq + qb - 1) / qb) * BH;
     const int64_t nkb = (Nk + PHX_FA_BC - 1) / PHX_FA_BC;
@@ -488,7 +483,11 @@ int launch_flash_split(phx_kernel k, const Desc *t, int rank, int64_t BH, int64_
     void *ws = nullptr;
     hipError_t e = hipMallocAsync(&ws, flash_split_bytes(BH, Nq, sp), s);
     if (e != hipSuccess) return hip_error(e, "hipMallocAsync(split-key workspace)");
-    int rc = launch_flash_split_ws(k, t, rank, BH, Nq, Nk, scale, sp, s, (uint64_t)(uintptr_t)ws);
+    hipFunction_t fs, fc;
+    int rc = flash_split_functions(k, &fs, &fc);
+    if (!rc)
+        rc = launch_flash_split_ws(k, t, rank, BH, Nq, Nk, scale, sp, s, (uint64_t)(uintptr_t)ws,
+                                   fs, fc);
     e = hipFreeAsync(ws, s);
     if (rc) return rc;
     if (e != hipSuccess) return hip_error(e, "hipFreeAsync(split-key workspace)");
@@ -675,7 +674,7 @@ extern "C" {
 
 const char *phx_last_error(void) { return g_err.c_str(); }
 
-int phx_init(int device, const char *dir) {
+static int init_device(int device, const char *dir) {
     hipError_t e = hipSetDevice(device);
     if (e != hipSuccess) return hip_error(e, "hipSetDevice");
     e = hipFree(nullptr);  // force context creation
@@ -687,6 +686,13 @@ int phx_init(int device, const char *dir) {
     g.dir = dir ? std::string(dir) : default_dir();
     g.init = true;
     return PHX_OK;
+}
+
+// The device set-up, then that of the allocation-free entry point
+// (phx_scratch.hip), which loads functions and so needs the lock released.
+int phx_init(int device, const char *dir) {
+    if (int rc = init_device(device, dir)) return rc;
+    return scratch_setup(device);
 }
 
 int phx_shutdown(void) {

@@ -144,6 +144,7 @@ def lib():
                                       _i64, ctypes.c_float]
     L.phx_flash_attention_bh.argtypes = [_vp, ctypes.c_int, _u64, _u64, _u64, _u64, _i64, _i64,
                                          _i64, _i64, ctypes.c_float]
+    L.phx_flash_attention_bh_noalloc.argtypes = L.phx_flash_attention_bh.argtypes
     L.phx_size_class.argtypes = [_sz]
     L.phx_size_class.restype = _sz
     L.phx_arena_create.argtypes = [ctypes.POINTER(_vp), _sz]
