@@ -86,6 +86,9 @@ def parse():
                          + ", ".join(BENCHES))
     ap.add_argument("--autotune", default=None, metavar="SPEC",
                     help="phobos-bench's tile pins; refused here: these kernels have one tiling each")
+    ap.add_argument("--shapes", action="store_true",
+                    help="only time the non-BASELINE shapes that run split (GEMMs at 512^3 and "
+                         "1024^3, one-head flash at 4096 queries, through the .ph entries) and exit")
     args = ap.parse_args()
     if args.bench is not None:
         # phobos-bench/src/main.rs:62-67, 109-115: one name from the list
@@ -95,7 +98,8 @@ def parse():
     if args.autotune is not None:
         ap.error("--autotune pins the reference's TILE_M/TILE_N/TILE_K/BR/BC search; the MI355X "
                  "kernels have one tiling each (GEMM 256x256, K step 32; flash 128 or 256 "
-                 "queries x 64 keys) and no search to pin")
+                 "queries x 64 keys) and no search to pin; problems too small to fill the GPU "
+                 "are split over K or over the keys instead (phx_split_plan)")
     return args
 
 
@@ -192,6 +196,54 @@ def setup(px, stream, wanted):
         ks.append(kk)
     px.synchronize()
     return ks
+
+
+def shapes_leg(px, stream, reps=20):
+    """Time the shapes that run split (phx_split_plan): each GEMM at 512^3 and
+    1024^3, and the one-head flash .ph entry (main.rs:334-371) at 4096 x 4096.
+    Inputs as in the BASELINE configs, average of `reps` launches after 3."""
+    out = []
+    ev0, ev1 = px.Event(), px.Event()
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        ev0.record(stream)
+        for _ in range(reps):
+            fn()
+        ev1.record(stream)
+        ev1.synchronize()
+        return ev0.elapsed_ms(ev1) / reps
+
+    for name, kid, esz in (("gemm_fp32", px.GEMM_FP32, 4),
+                           ("gemm_fp16tc_fp32acc", px.GEMM_FP16TC_FP32ACC, 4),
+                           ("gemm_fp16", px.GEMM_FP16, 2)):
+        for n in (512, 1024):
+            a = px.normal_f32(1, n * n, 1 / np.sqrt(n))
+            b = px.normal_f32(2, n * n, 1 / np.sqrt(n))
+            if esz == 2:
+                a, b = px.to_f16_bits(a), px.to_f16_bits(b)
+            da, db = px.DeviceBuffer.from_array(a), px.DeviceBuffer.from_array(b)
+            dc = px.DeviceBuffer(n * n * esz)
+            dc.zero(stream)
+            ms = timed(lambda: px.launch_gemm(stream, kid, da, db, dc, n, n, n, 1.0, 0.0))
+            sp, ws = px.split_plan(kid, [n, n, n])
+            out.append({"kernel": name, "shape": [n, n, n], "splits": sp, "workspace_bytes": ws,
+                        "us": round(ms * 1e3, 2),
+                        "tflops": round((2 * n ** 3 + n * n) / (ms / 1e3) / 1e12, 2)})
+    S, D = 4096, 64
+    for name, kid, esz in (("flash_fp32", px.FLASH_FP32, 4), ("flash_fp16", px.FLASH_FP16, 2)):
+        ts = [px.normal_f32(sd, S * D) for sd in (1, 2, 3)]
+        if esz == 2:
+            ts = [px.to_f16_bits(t) for t in ts]
+        q, k, v = (px.DeviceBuffer.from_array(t) for t in ts)
+        o = px.DeviceBuffer(S * D * esz)
+        ms = timed(lambda: px.launch_flash(stream, kid, q, k, v, o, S, S, D, 0.125))
+        sp, ws = px.split_plan(kid, [S, S, D])
+        out.append({"kernel": name + " (one head)", "shape": [S, S, D], "splits": sp,
+                    "workspace_bytes": ws, "us": round(ms * 1e3, 2),
+                    "tflops": round(4 * S * S * D / (ms / 1e3) / 1e12, 2)})
+    return out
 
 
 def cpu_baseline(seconds):
@@ -401,6 +453,13 @@ def main():
         return
     info = px.device_info()
     log(f"device: {info}")
+    if args.shapes:
+        res = shapes_leg(px, px.Stream())
+        for r in res:
+            log(f"{r['kernel']:28s} {str(r['shape']):18s} splits {r['splits']:2d}  "
+                f"{r['us']:8.2f} us  {r['tflops']:8.2f} TFLOP/s")
+        print(json.dumps({"shapes": res, "device": info}), flush=True)
+        return
     all_names = ["saxpy_fp32", "gemm_fp32", "gemm_fp16tc_fp32acc", "gemm_fp16", "flash_fp32",
                  "flash_fp16"]
     wanted = all_names if args.kernels == "all" else args.kernels.split(",")
