@@ -534,11 +534,14 @@ __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp
 // ---------------------------------------------------------------- f32 path
 // V^T rows are stored 4 apart by one instruction (the register transpose,
 // rows 4dq + r) and read 16 consecutive at a time (the MFMA operands): XOR
-// the chunk with (row ^ row>>2) & 15, a bijection on both row sets.  With
-// row & 15 the stores hit each bank 4 ways (measured on gfx950: 96.6 vs 73.5
-// cycles per ds_write_b128 in a one-wave loop; reads 61.3 vs 58.2).
+// the chunk with ((row >> 2) ^ (row << 2)) & 15, i.e. the row's two 2-bit
+// fields swapped.  SQ_LDS_BANK_CONFLICT reads 0 for both access sets with
+// it on gfx950 (LDS microbenchmark of exactly these two patterns); row & 15
+// costs the stores 24 conflict cycles per instruction, and (row ^ row>>2) & 15
+// costs the reads 4, although both map each 16-lane group to 16 distinct
+// 16-byte slots.
 __device__ __forceinline__ uint32_t vt_off(uint32_t row, uint32_t chunk) {
-    return row * ROW_BYTES + ((chunk ^ ((row ^ (row >> 2)) & 15)) << 4);
+    return row * ROW_BYTES + ((chunk ^ (((row >> 2) ^ (row << 2)) & 15)) << 4);
 }
 // K rows / V^T rows are 64 floats (256 B, 16 chunks).  K is copied global ->
 // LDS directly (buffer_load ... lds: a 64-lane copy fills 4 rows; lane l lands

@@ -32,4 +32,5 @@ int launch_flash_split_ws(phx_kernel k, const Desc *t, int rank, int64_t BH, int
                           hipFunction_t fs, hipFunction_t fc);
 // the allocation-free entry point's per-device set-up (phx_scratch.hip)
 int scratch_setup(int device);
+void scratch_reset();
 }  // namespace phx

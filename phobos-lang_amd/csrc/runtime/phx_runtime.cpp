@@ -696,6 +696,7 @@ int phx_init(int device, const char *dir) {
 }
 
 int phx_shutdown(void) {
+    scratch_reset();
     std::lock_guard<std::mutex> lock(g.mu);
     for (auto &kv : g.modules) (void)hipModuleUnload(kv.second);
     g.modules.clear();

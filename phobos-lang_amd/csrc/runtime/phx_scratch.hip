@@ -17,6 +17,7 @@
 #include "phx_internal.h"
 
 #include <cstring>
+#include <string>
 
 namespace phx {
 
@@ -27,8 +28,10 @@ static __device__ __align__(256) char scratch[PHX_SCRATCH_BYTES];
 constexpr int kMaxDevices = 64;
 static uint64_t g_scratch[kMaxDevices];
 // Functions the entry point launches, resolved at set-up so that a call
-// loads no code object (a load allocates device memory).
+// loads no code object (a load allocates device memory).  Null when the
+// code objects lack them; the entry point then reports PHX_E_NOT_FOUND.
 static hipFunction_t g_bh[2], g_split[2], g_combine[2];  // [0]: f16, [1]: f32
+static std::string g_missing;  // why a function could not be resolved
 
 int scratch_setup(int device) {
     if (device < 0 || device >= kMaxDevices)
@@ -39,11 +42,20 @@ int scratch_setup(int device) {
     if (e != hipSuccess) return hip_error(e, "hipGetSymbolAddress(scratch)");
     g_scratch[device] = (uint64_t)(uintptr_t)p;
     const phx_kernel bh[2] = {PHX_FLASH_FP16_BH, PHX_FLASH_FP32_BH};
+    g_missing.clear();
     for (int i = 0; i < 2; ++i) {
-        if (int rc = builtin(bh[i], &g_bh[i])) return rc;
-        if (int rc = flash_split_functions(bh[i], &g_split[i], &g_combine[i])) return rc;
+        if (builtin(bh[i], &g_bh[i]) ||
+            flash_split_functions(bh[i], &g_split[i], &g_combine[i])) {
+            g_bh[i] = g_split[i] = g_combine[i] = nullptr;
+            g_missing = phx_last_error();  // the other entry points report it on use
+        }
     }
     return PHX_OK;
+}
+
+void scratch_reset() {  // phx_shutdown: the functions are unloaded
+    for (int i = 0; i < 2; ++i) g_bh[i] = g_split[i] = g_combine[i] = nullptr;
+    for (auto &p : g_scratch) p = 0;
 }
 
 }  // namespace phx
@@ -65,6 +77,8 @@ extern "C" int phx_flash_attention_bh_noalloc(phx_stream s, phx_kernel k, uint64
     if (dev < 0 || dev >= kMaxDevices || !g_scratch[dev])
         return set_error(PHX_E_NOT_INIT, "phx_init has not set up device %d", dev);
     const int i = k == PHX_FLASH_FP16_BH ? 0 : 1;
+    if (!g_bh[i] || !g_split[i] || !g_combine[i])
+        return set_error(PHX_E_NOT_FOUND, "flash_attention_bh_noalloc: %s", g_missing.c_str());
     const int sp = flash_split(k, BH, Nq, Nk);
     if (sp > 1) {
         const size_t need = flash_split_bytes(BH, Nq, sp);
