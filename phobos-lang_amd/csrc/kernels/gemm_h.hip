@@ -725,3 +725,216 @@ extern "C" __global__ __launch_bounds__(256) void gemm_splitk_reduce(const float
                                                                       float alpha, float beta) {
     phx_splitk_reduce(W, S, C, ldc, M, N, alpha, beta);
 }
+
+#ifdef PHX_GEMM_TC
+// ---------------------------------------------------- eight-wave tc kernel
+// gemm_w8: the whole-tile gemm_fp16tc_fp32acc (M, N multiples of 256, K of
+// 32) with two waves per SIMD.  The one-wave-per-SIMD kernel above issues
+// its f32 operand loads and its MFMAs from one instruction stream; when the
+// CU's load path is saturated (64 KiB of f32 per K step, as many cycles as
+// the step's MFMAs) a load that cannot issue holds up the MFMAs behind it,
+// and the two run one after the other.  A microbenchmark on MI355X (one
+// workgroup per CU, L2-resident data, the tc per-step load volume and MFMA
+// count): 244 us with one wave per SIMD doing both, against 178 us with two
+// waves per SIMD (either split into a loading and a computing wave, or both
+// doing half of each), where MFMA-only runs 127 us and loads-only 160 us.
+// So here 8 waves own 128 x 64 of the 256 x 256 tile each (4 x 2
+// v_mfma_f32_32x32x16_f16 tiles, 128 f32 accumulators), every wave loads
+// and converts its share of the operands, and a stalled load in one wave
+// leaves the SIMD to the other wave's MFMAs.  Three LDS stages and one
+// register set of f32 loads (248 VGPRs per wave); one barrier per step.
+// Measured at 4096^3: 130-135 us against 139-142 us for the one-wave kernel
+// (same box, alternating), bit-identical output.  Probe builds put the rest
+// on the load path: without the MFMAs 105 us, without the loads 90 us.
+#define W8_NT 512
+#define W8_WM 128
+#define W8_WN 64
+
+struct Frags8 {
+    phx_h8 a[4];
+    phx_h8 b[2];
+};
+struct Regs8 {
+    Chunk a[2];
+    Chunk b[2];
+};
+
+__device__ __forceinline__ void w8_mfma(phx_f16v (&acc)[4][2], const Frags8 &f, int m) {
+    acc[m >> 1][m & 1] =
+        __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[m >> 1], f.b[m & 1], acc[m >> 1][m & 1], 0, 0, 0);
+}
+
+// operand read r of a slice: 0-3 the A fragments, 4-5 the B fragments
+__device__ __forceinline__ void w8_read(Frags8 &f, const char *stage, uint32_t s, uint32_t wm,
+                                        uint32_t wn, uint32_t lane, int r) {
+    if (r < 4) {
+        f.a[r] = *(const phx_h8 *)(stage + a_off(wm + r * 32 + (lane & 31), 2 * s + (lane >> 5)));
+    } else {
+        Frags tmp;
+        read_b(tmp, stage, s, wn, lane, r - 4);
+        f.b[r - 4] = tmp.b[r - 4];
+    }
+}
+
+// Thread t's chunks of a step: A chunk i = row 128 i + t/4, k chunk t%4;
+// B chunk i = k row 16 i + t/32, n chunk t%32.  Each chunk is 8 f32 (two
+// 16-byte loads), rounded to one 16-byte f16 chunk in LDS.
+__device__ __forceinline__ void w8_load_a(Regs8 &R, __amdgpu_buffer_rsrc_t ra, uint32_t voa,
+                                          uint32_t lda, int i) {
+    R.a[i] = load_chunk(ra, voa, (int)((uint32_t)(i * 128 * lda) * ESZ));
+}
+__device__ __forceinline__ void w8_load_b(Regs8 &R, __amdgpu_buffer_rsrc_t rb, uint32_t vob,
+                                          uint32_t ldb, int i) {
+    R.b[i] = load_chunk(rb, vob, (int)((uint32_t)(i * 16 * ldb) * ESZ));
+}
+__device__ __forceinline__ void w8_store_a(const Regs8 &R, char *stage, uint32_t tid, int i) {
+    *(phx_u4 *)(stage + a_off(i * 128 + (tid >> 2), tid & 3)) = pack(R.a[i]);
+}
+__device__ __forceinline__ void w8_store_b(const Regs8 &R, char *stage, uint32_t tid, int i) {
+    *(phx_u4 *)(stage + A_BYTES + b_off(i * 16 + (tid >> 5), tid & 31)) = pack(R.b[i]);
+}
+
+// One K step kt over three LDS stages: cur holds step kt, nxt step kt+1,
+// and fill receives step kt+2, converted from R while step kt+3's loads are
+// issued into R (the data of step kt+2 was loaded during step kt-1).  First
+// half: slice 0's MFMAs (F0) with slice 1's operand reads (into F1) and A's
+// two chunks; the barrier; second half: slice 1's MFMAs with the next
+// step's slice-0 reads (from nxt, into F0) and B's two chunks.  fill was
+// last read during step kt-1, before the barrier of that step.
+__device__ __forceinline__ void w8_chunk(Regs8 &R, char *fill, __amdgpu_buffer_rsrc_t ra,
+                                         __amdgpu_buffer_rsrc_t rb, uint32_t voa, uint32_t vob,
+                                         uint32_t lda, uint32_t ldb, uint32_t tid, int c) {
+    if (c < 2) {
+        w8_store_a(R, fill, tid, c);
+        w8_load_a(R, ra, voa, lda, c);
+    } else {
+        w8_store_b(R, fill, tid, c - 2);
+        w8_load_b(R, rb, vob, ldb, c - 2);
+    }
+}
+
+__device__ __forceinline__ void w8_step(phx_f16v (&acc)[4][2], Frags8 &F0, Frags8 &F1,
+                                        const char *cur, const char *nxt, char *fill, Regs8 &R,
+                                        const TIn *A, uint32_t lda, const TIn *B, uint32_t ldb,
+                                        uint32_t K, uint32_t m0, uint32_t n0, uint32_t kt,
+                                        uint32_t voa, uint32_t vob, uint32_t wm, uint32_t wn,
+                                        uint32_t tid, uint32_t lane) {
+    const uint32_t kn = (kt + 3) * BK;  // the step whose data the reloads fetch
+    const __amdgpu_buffer_rsrc_t ra = a_rsrc<false>(A, lda, 0, K, m0, kn);
+    const __amdgpu_buffer_rsrc_t rb = b_rsrc<false>(B, ldb, 0, K, n0, kn);
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+        w8_mfma(acc, F0, m);
+        if (m < 6) w8_read(F1, cur, 1, wm, wn, lane, m);
+        if (m == 0 || m == 2) w8_chunk(R, fill, ra, rb, voa, vob, lda, ldb, tid, m >> 1);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    PHX_WAIT_VM_LGKM0(63);  // this wave's F1 reads and fill stores are done
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+        w8_mfma(acc, F1, m);
+        if (m < 6) w8_read(F0, nxt, 0, wm, wn, lane, m);
+        if (m == 1 || m == 5) w8_chunk(R, fill, ra, rb, voa, vob, lda, ldb, tid, 2 + (m >> 2));
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+#define W8S(CUR, NXT, FILL, KT)                                                               \
+    w8_step(acc, F0, F1, CUR, NXT, FILL, R, A, lda, B, ldb, (uint32_t)K, m0, n0, KT, voa, vob, \
+            wm, wn, tid, lane)
+extern "C" __global__ __launch_bounds__(W8_NT, 1) void gemm_w8(PHX_MEMREF2(TIn, a, int64_t),
+                                                                PHX_MEMREF2(TIn, b, int64_t),
+                                                                PHX_MEMREF2(TOut, c, int64_t),
+                                                                float alpha, float beta) {
+    __shared__ __attribute__((aligned(16))) char stg[3 * STAGE_BYTES];
+    const int64_t M = a_s0, K = a_s1, N = b_s1;
+    if (blockDim.x != W8_NT || M % BM || N % BN || K % BK || M <= 0 || N <= 0 || K <= 0 ||
+        b_s0 != K || c_s0 != M || c_s1 != N || a_st1 != 1 || b_st1 != 1 || c_st1 != 1 ||
+        a_st0 % PHX_TC_K_MULT || (b_st0 | c_st0) % PHX_TC_N_MULT || M > INT32_MAX ||
+        (BM + 1) * (a_st0 > b_st0 ? a_st0 : b_st0) * (int64_t)sizeof(TIn) > INT32_MAX ||
+        ((uintptr_t)(a_ptr + a_off) | (uintptr_t)(b_ptr + b_off) | (uintptr_t)(c_ptr + c_off)) & 15)
+        return;
+    const TIn *A = a_ptr + a_off;
+    const TIn *B = b_ptr + b_off;
+    TOut *C = c_ptr + c_off;
+    const uint32_t lda = (uint32_t)a_st0, ldb = (uint32_t)b_st0;
+    const int64_t ldc = c_st0;
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t wm = (wave >> 2) * W8_WM, wn = (wave & 3) * W8_WN;
+    const uint32_t tiles_n = (uint32_t)(N / BN), tiles_m = (uint32_t)(M / BM);
+    const uint32_t ntiles = tiles_m * tiles_n, nblk = phx_block_count();
+    const uint32_t nk = (uint32_t)(K / BK);
+    const uint32_t voa = ((tid >> 2) * lda + (tid & 3) * 8) * ESZ;
+    const uint32_t vob = ((tid >> 5) * ldb + (tid & 31) * 8) * ESZ;
+    char *const S0 = stg, *const S1 = stg + STAGE_BYTES, *const S2 = stg + 2 * STAGE_BYTES;
+
+    for (uint32_t t = phx_block_linear(); t < ntiles; t += nblk) {
+        const uint32_t ts = nblk == ntiles ? phx_xcd_swizzle(t, ntiles) : t;
+        const uint32_t gsz = GROUP_M * tiles_n;
+        const uint32_t g0 = (ts / gsz) * GROUP_M;
+        const uint32_t gm = (tiles_m - g0) < GROUP_M ? (tiles_m - g0) : GROUP_M;
+        const uint32_t m0 = (g0 + (ts % gsz) % gm) * BM, n0 = ((ts % gsz) / gm) * BN;
+
+        phx_f16v acc[4][2];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                acc[i][j] = (phx_f16v){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+        Frags8 F0, F1;
+        Regs8 R;
+        {   // prologue: steps 0 and 1 into stages 0 and 1, step 2 in flight in R
+            for (int p = 0; p < 3; ++p) {
+                const __amdgpu_buffer_rsrc_t ra = a_rsrc<false>(A, lda, 0, (uint32_t)K, m0, p * BK);
+                const __amdgpu_buffer_rsrc_t rb = b_rsrc<false>(B, ldb, 0, (uint32_t)K, n0, p * BK);
+                char *prev = stg + (p - 1) * STAGE_BYTES;  // step p-1's stage
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    if (p > 0) w8_store_a(R, prev, tid, i);
+                    w8_load_a(R, ra, voa, lda, i);
+                    if (p > 0) w8_store_b(R, prev, tid, i);
+                    w8_load_b(R, rb, vob, ldb, i);
+                }
+            }
+        }
+        PHX_WAIT_VM_LGKM0(63);
+        __builtin_amdgcn_s_barrier();
+#pragma unroll
+        for (int r = 0; r < 6; ++r) w8_read(F0, S0, 0, wm, wn, lane, r);
+        uint32_t kt = 0;
+        for (; kt + 3 <= nk; kt += 3) {
+            W8S(S0, S1, S2, kt);
+            W8S(S1, S2, S0, kt + 1);
+            W8S(S2, S0, S1, kt + 2);
+        }
+        if (kt < nk) W8S(S0, S1, S2, kt);
+        if (kt + 1 < nk) W8S(S1, S2, S0, kt + 1);
+        PHX_WAIT_VMCNT(0);  // the loads past K (zeros) before the stages are reused
+        __syncthreads();
+
+        // epilogue: C = fl(fl(alpha*acc) + fl(beta*c)), C not read when
+        // beta == 0.  Lane l holds column 32j + l%32 and rows
+        // 32i + 8(r/4) + 4(l/32) + r%4 of the wave's 128 x 64 block; a store
+        // writes two 128-byte row segments.
+        const uint32_t lrow = 4 * (lane >> 5), lcol = lane & 31;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int64_t row = m0 + wm + 32 * i + 8 * (r >> 2) + lrow + (r & 3);
+                    TOut *dst = C + row * ldc + n0 + wn + 32 * j + lcol;
+                    float o = alpha * acc[i][j][r];
+                    if (beta != 0.0f) {
+                        const float cb = beta * *dst;
+                        o = o + cb;
+                    }
+                    *dst = o;
+                }
+    }
+}
+#endif

@@ -361,6 +361,15 @@ int gemm_split(phx_kernel k, int64_t M, int64_t N, int64_t K) {
     return (int)((steps + per - 1) / per);
 }
 
+// Whether a gemm_fp16tc_fp32acc launch runs the eight-wave kernel gemm_w8
+// (whole 256 x 256 tiles and 32-deep K steps); PHX_TC_W8=0 in the
+// environment turns it off, for measurement.
+static bool tc_w8(int64_t M, int64_t N, int64_t K) {
+    if (const char *env = getenv("PHX_TC_W8"))
+        if (atoi(env) == 0) return false;
+    return M % PHX_H_BM == 0 && N % PHX_H_BN == 0 && K % PHX_H_BK == 0;
+}
+
 // K columns per chunk of a split into sp chunks (a multiple of 32).
 static int64_t split_chunk(int64_t K, int sp) {
     const int64_t steps = (K + PHX_SPLIT_KSTEP - 1) / PHX_SPLIT_KSTEP;
@@ -514,6 +523,15 @@ int launch_raw(hipFunction_t f, const uint32_t grid[3], const uint32_t block[3],
                 memcpy(&alpha, args[21], 4);
                 memcpy(&beta, args[22], 4);
                 return launch_gemm_split((phx_kernel)k, t, d[0], d[1], d[2], alpha, beta, sp, s);
+            }
+            if (k == PHX_GEMM_FP16TC_FP32ACC && tc_w8(d[0], d[1], d[2])) {
+                hipFunction_t fw;
+                if (int rc = aux_function(kSpecs[k].file, "gemm_w8", &fw)) return rc;
+                const uint32_t tiles = (uint32_t)((d[0] / PHX_H_BM) * (d[1] / PHX_H_BN));
+                hipError_t e = hipModuleLaunchKernel(fw, tiles, 1, 1, PHX_TC_W8_THREADS, 1, 1, 0,
+                                                     s, args, nullptr);
+                if (e != hipSuccess) return hip_error(e, "hipModuleLaunchKernel(gemm_w8)");
+                return PHX_OK;
             }
         }
         if (k == PHX_FLASH_FP16 || k == PHX_FLASH_FP32 || k == PHX_FLASH_FP16_BH ||
