@@ -727,7 +727,7 @@ extern "C" __global__ __launch_bounds__(256) void gemm_splitk_reduce(const float
 }
 
 #ifdef PHX_GEMM_TC
-// ---------------------------------------------------- eight-wave tc kernel
+// ------------------------------------------------- eight-wave tc kernel
 // gemm_w8: the whole-tile gemm_fp16tc_fp32acc (M, N multiples of 256, K of
 // 32) with two waves per SIMD.  The one-wave-per-SIMD kernel above issues
 // its f32 operand loads and its MFMAs from one instruction stream; when the
@@ -754,14 +754,35 @@ struct Frags8 {
     phx_h8 a[4];
     phx_h8 b[2];
 };
-struct Regs8 {
-    Chunk a[2];
-    Chunk b[2];
-};
 
 __device__ __forceinline__ void w8_mfma(phx_f16v (&acc)[4][2], const Frags8 &f, int m) {
     acc[m >> 1][m & 1] =
         __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[m >> 1], f.b[m & 1], acc[m >> 1][m & 1], 0, 0, 0);
+}
+
+// C = fl(fl(alpha*acc) + fl(beta*c)) over a wave's 128 x 64 block at (r0,
+// c0), rounded once to the output type; C is not read when beta == 0.  Lane
+// l holds column 32j + l%32 and rows 32i + 8(r/4) + 4(l/32) + r%4; a store
+// writes two row segments of 32 elements.
+__device__ __forceinline__ void w8_epilogue(const phx_f16v (&acc)[4][2], TOut *C, int64_t ldc,
+                                            uint32_t r0, uint32_t c0, float alpha, float beta,
+                                            uint32_t lane) {
+    const uint32_t lrow = 4 * (lane >> 5), lcol = lane & 31;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int64_t row = r0 + 32 * i + 8 * (r >> 2) + lrow + (r & 3);
+                TOut *dst = C + row * ldc + c0 + 32 * j + lcol;
+                float o = alpha * acc[i][j][r];
+                if (beta != 0.0f) {
+                    const float cb = beta * (float)*dst;
+                    o = o + cb;
+                }
+                *dst = (TOut)o;
+            }
 }
 
 // operand read r of a slice: 0-3 the A fragments, 4-5 the B fragments
@@ -769,12 +790,29 @@ __device__ __forceinline__ void w8_read(Frags8 &f, const char *stage, uint32_t s
                                         uint32_t wn, uint32_t lane, int r) {
     if (r < 4) {
         f.a[r] = *(const phx_h8 *)(stage + a_off(wm + r * 32 + (lane & 31), 2 * s + (lane >> 5)));
-    } else {
-        Frags tmp;
-        read_b(tmp, stage, s, wn, lane, r - 4);
-        f.b[r - 4] = tmp.b[r - 4];
+    } else {  // B columns wn + 32j + lane%32 through two transposing reads
+        const int j = r - 4;
+        const char *Bs = stage + A_BYTES;
+        const uint32_t q = lane >> 4, sl = lane & 15;
+        const uint32_t col = wn + j * 32 + 16 * (q & 1) + 4 * (sl & 3);
+        phx_fp16x4 h[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const uint32_t row = 16 * s + 8 * (q >> 1) + 4 * t + (sl >> 2);
+            const uint32_t off = b_off(row, col >> 3) + ((col & 7) << 1);
+            h[t] = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                (phx_lds_h4p)((__attribute__((address_space(3))) char *)(Bs + off)));
+        }
+        const phx_h4 lo = __builtin_bit_cast(phx_h4, h[0]);
+        const phx_h4 hi = __builtin_bit_cast(phx_h4, h[1]);
+        f.b[j] = (phx_h8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     }
 }
+
+struct Regs8 {
+    Chunk a[2];
+    Chunk b[2];
+};
 
 // Thread t's chunks of a step: A chunk i = row 128 i + t/4, k chunk t%4;
 // B chunk i = k row 16 i + t/32, n chunk t%32.  Each chunk is 8 f32 (two
@@ -915,26 +953,7 @@ extern "C" __global__ __launch_bounds__(W8_NT, 1) void gemm_w8(PHX_MEMREF2(TIn, 
         PHX_WAIT_VMCNT(0);  // the loads past K (zeros) before the stages are reused
         __syncthreads();
 
-        // epilogue: C = fl(fl(alpha*acc) + fl(beta*c)), C not read when
-        // beta == 0.  Lane l holds column 32j + l%32 and rows
-        // 32i + 8(r/4) + 4(l/32) + r%4 of the wave's 128 x 64 block; a store
-        // writes two 128-byte row segments.
-        const uint32_t lrow = 4 * (lane >> 5), lcol = lane & 31;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int64_t row = m0 + wm + 32 * i + 8 * (r >> 2) + lrow + (r & 3);
-                    TOut *dst = C + row * ldc + n0 + wn + 32 * j + lcol;
-                    float o = alpha * acc[i][j][r];
-                    if (beta != 0.0f) {
-                        const float cb = beta * *dst;
-                        o = o + cb;
-                    }
-                    *dst = o;
-                }
+        w8_epilogue(acc, C, ldc, m0 + wm, n0 + wn, alpha, beta, lane);
     }
 }
 #endif

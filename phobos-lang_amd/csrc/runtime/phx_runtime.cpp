@@ -362,10 +362,14 @@ int gemm_split(phx_kernel k, int64_t M, int64_t N, int64_t K) {
 }
 
 // Whether a gemm_fp16tc_fp32acc launch runs the eight-wave kernel gemm_w8
-// (whole 256 x 256 tiles and 32-deep K steps); PHX_TC_W8=0 in the
-// environment turns it off, for measurement.
-static bool tc_w8(int64_t M, int64_t N, int64_t K) {
-    if (const char *env = getenv("PHX_TC_W8"))
+// (whole 256 x 256 tiles and 32-deep K steps).  gemm_fp16, whose operand
+// copies are half the bytes and already overlap its MFMAs, measured the
+// same with an eight-wave form (114-119 vs 115-118 us) and keeps its
+// one-wave kernel.  PHX_GEMM_W8=0 in the environment turns it off, for
+// measurement.
+static bool gemm_w8(phx_kernel k, int64_t M, int64_t N, int64_t K) {
+    if (k != PHX_GEMM_FP16TC_FP32ACC) return false;
+    if (const char *env = getenv("PHX_GEMM_W8"))
         if (atoi(env) == 0) return false;
     return M % PHX_H_BM == 0 && N % PHX_H_BN == 0 && K % PHX_H_BK == 0;
 }
@@ -524,7 +528,7 @@ int launch_raw(hipFunction_t f, const uint32_t grid[3], const uint32_t block[3],
                 memcpy(&beta, args[22], 4);
                 return launch_gemm_split((phx_kernel)k, t, d[0], d[1], d[2], alpha, beta, sp, s);
             }
-            if (k == PHX_GEMM_FP16TC_FP32ACC && tc_w8(d[0], d[1], d[2])) {
+            if (gemm_w8((phx_kernel)k, d[0], d[1], d[2])) {
                 hipFunction_t fw;
                 if (int rc = aux_function(kSpecs[k].file, "gemm_w8", &fw)) return rc;
                 const uint32_t tiles = (uint32_t)((d[0] / PHX_H_BM) * (d[1] / PHX_H_BN));

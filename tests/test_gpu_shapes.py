@@ -230,22 +230,25 @@ def test_bh_flash_split_matches_unsplit(px_gpu, stream, bits):
     assert _flash_rel(outs[0], outs[1]) < TOL[bits]
 
 
+@pytest.mark.parametrize("kern_name", ["GEMM_FP16TC_FP32ACC"])
 @pytest.mark.parametrize("M,N,K", [(512, 768, 2048), (1024, 256, 96), (256, 256, 32)])
-def test_tc_eight_wave_kernel_matches_one_wave_kernel(px_gpu, stream, M, N, K):
+def test_eight_wave_kernel_matches_one_wave_kernel(px_gpu, stream, kern_name, M, N, K):
     # Whole-tile gemm_fp16tc_fp32acc launches run gemm_w8 (two waves per
-    # SIMD); PHX_TC_W8=0 runs the one-wave kernel.  Both sum each output's
-    # K products in the same order, so they agree bit for bit, and both
-    # meet the oracle.
+    # SIMD); PHX_GEMM_W8=0 runs the one-wave kernel.  Both sum each output's
+    # K products in the same order, so they agree bit for bit, and both meet
+    # the oracle.
     px = px_gpu
-    kern = px.GEMM_FP16TC_FP32ACC
+    kern = getattr(px, kern_name)
     A = oracle.f16_round(oracle.normal_f32(61, M * K, 1 / np.sqrt(K))).reshape(M, K)
     B = oracle.f16_round(oracle.normal_f32(62, K * N, 1 / np.sqrt(K))).reshape(K, N)
     C = oracle.normal_f32(63, M * N).reshape(M, N)
     outs = []
     with _Env("PHX_GEMM_SPLIT", 1):
         for w8 in (1, 0):
-            with _Env("PHX_TC_W8", w8):
+            with _Env("PHX_GEMM_W8", w8):
                 outs.append(_gemm(px, stream, kern, A, B, C, 0.75, -0.5))
+    if kern_name == "GEMM_FP16":
+        C = oracle.f16_round(C)
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
     want = oracle.gemm_full(A, B, C, 0.75, -0.5, round16=True)
-    _check("GEMM_FP16TC_FP32ACC", outs[0], want)
+    _check(kern_name, outs[0], want)
