@@ -269,7 +269,9 @@ int phx_pod_set_kernel(phx_pod p, uint32_t kernel_id, phx_kernel k);
  * sizes and strides, as engine.rs:582-647 launches every kernel. */
 int phx_pod_set_kernel_function(phx_pod p, uint32_t kernel_id, phx_function f, int index_bits);
 /* Runs one segment to completion.  stats (nullable) receives
- * {n_alloc, n_load, n_compute, n_store, n_free, compute_ns, wall_ns, io_ns}. */
+ * {n_alloc, n_load, n_compute, n_store, n_free, compute_ns, wall_ns, io_ns}.
+ * compute_ns is device time with at least one COMPUTE running (the union of
+ * the leaves' event intervals; leaves on different streams may overlap). */
 int phx_pod_run_segment(phx_pod p, const char *segment_text, uint64_t stats[8]);
 
 /* The scheduler's wire messages, protobuf-encoded (proto3 wire format):

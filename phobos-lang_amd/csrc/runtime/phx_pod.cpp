@@ -15,15 +15,19 @@
 //   * LOAD / STORE move f32 regions of file:// tensors (storage.rs:22-79).
 //
 // MI355X design: the reference does a blocking file read then a synchronous
-// cuMemcpy on the engine thread (tile_store.rs:153-181).  Here file I/O runs
-// on a worker pool into pinned (hipHostMalloc) staging slabs, and the copy is
-// a hipMemcpyAsync on a dedicated copy stream, so LOADs of later supertiles,
-// STOREs of finished ones and COMPUTEs overlap.  Built-in leaf kernels get
-// their grid from phx_grid_for (the reference's leaf grid would also be
+// cuMemcpy on the engine thread (tile_store.rs:153-181).  Here a LOAD or
+// STORE moves in chunks through a bounded pool of pinned (hipHostMalloc)
+// staging buffers: file reads and writes run on a worker pool, the copies
+// are hipMemcpyAsync on two copy streams (one per direction), so reading
+// chunk c+1 overlaps copying chunk c, and LOADs of later supertiles, STOREs
+// of finished ones and COMPUTEs overlap.  The pool is allocated on first use
+// and kept for the pod's lifetime, so the pinned host memory is bounded
+// however large the segment.  Built-in leaf kernels get their grid from phx_grid_for (the reference's leaf grid would also be
 // correct: every kernel strides over its work).
 #include <fcntl.h>
 #include <unistd.h>
 
+#include <algorithm>
 #include <chrono>
 #include <condition_variable>
 #include <cstdio>
@@ -107,7 +111,24 @@ bool byte_spans(const std::vector<uint64_t> &tshape, const Region &r,
     return false;
 }
 
+// Staging chunk size and the most chunks a pod pins: 8 MiB x 32 by default;
+// PHX_POD_STAGE_MIB (1..1024) and PHX_POD_STAGE_CHUNKS (2..256) override.
+static size_t env_clamped(const char *name, size_t dflt, size_t lo, size_t hi) {
+    const char *e = getenv(name);
+    const long v = e ? atol(e) : (long)dflt;
+    return v < (long)lo ? lo : v > (long)hi ? hi : (size_t)v;
+}
+
 // Fixed worker pool for file I/O.
+// File reads and writes of LOAD/STORE run on a pool of host threads (the
+// reference runs each on tokio's blocking pool, engine.rs:437-440, 489-492).
+// Eight by default; PHX_POD_IO_THREADS (1..64) overrides.
+static int io_threads() {
+    const char *e = getenv("PHX_POD_IO_THREADS");
+    const int n = e ? atoi(e) : 8;
+    return n < 1 ? 1 : n > 64 ? 64 : n;
+}
+
 class IoPool {
    public:
     explicit IoPool(int n) {
@@ -161,7 +182,8 @@ uint64_t now_ns() {
 struct phx_pod_s {
     phx_arena arena = nullptr;
     std::vector<hipStream_t> streams;
-    hipStream_t copy_stream = nullptr;
+    hipStream_t copy_stream = nullptr;   // LOAD: host -> device
+    hipStream_t store_stream = nullptr;  // STORE: device -> host
     size_t next_stream = 0;
     std::unordered_map<uint32_t, TensorInfo> tensors;
     std::unordered_map<uint32_t, phx_kernel> kernels;
@@ -169,9 +191,10 @@ struct phx_pod_s {
     // gfx950 code object in place of PTX): function and index width
     std::unordered_map<uint32_t, std::pair<hipFunction_t, int>> functions;
     std::unordered_map<uint64_t, TileBuf> tiles;
-    // pinned staging slabs, keyed by byte size
-    std::multimap<size_t, void *> pinned_free;
-    std::vector<void *> pinned_all;
+    // pinned staging chunks of stage_bytes, at most stage_chunks of them
+    size_t stage_bytes = 0, stage_chunks = 0;
+    std::vector<void *> stage_free;
+    std::vector<void *> stage_all;
     IoPool *io = nullptr;
 };
 
@@ -179,20 +202,68 @@ namespace {
 
 struct Inflight {
     enum Stage { H2D, D2H, Kernel } stage;
-    size_t idx;  // instruction index
+    size_t idx;         // instruction index
+    size_t chunk = 0;   // H2D / D2H: chunk of the tile
     hipEvent_t start = nullptr, done = nullptr;
     void *staging = nullptr;
-    size_t staging_bytes = 0;
 };
 
+// A file read (LOAD) or write (STORE) of one chunk that a worker finished.
 struct IoDone {
-    size_t idx;
+    size_t idx, chunk;
     bool ok;
     std::string err;
     uint64_t ns;
-    void *staging;  // STORE: pinned slab to return once the file write is done
-    size_t bytes;
+    void *staging;
 };
+
+// A LOAD or STORE in progress: the tile's bytes in chunks of
+// the pod's staging size, each staged, copied and read or written on its own.
+struct Xfer {
+    bool load;
+    uint64_t dev;  // tile address
+    size_t bytes;  // tile bytes
+    size_t nchunks, next = 0, landed = 0;
+    std::string path;
+    std::vector<std::pair<uint64_t, size_t>> spans;  // (file byte offset, bytes), tile order
+};
+
+// Reads (or writes) tile bytes [a, a + len) from (to) their file spans.
+bool chunk_io(const Xfer &x, bool write, char *buf, size_t a, size_t len, std::string *err) {
+    int fd = write ? open(x.path.c_str(), O_RDWR | O_CREAT, 0644) : open(x.path.c_str(), O_RDONLY);
+    if (fd < 0) {
+        *err = (write ? "cannot open/write " : "cannot open/read ") + x.path;
+        return false;
+    }
+    size_t pos = 0;  // tile byte where the current span starts
+    bool ok = true;
+    for (auto &sp : x.spans) {
+        const size_t s0 = pos;
+        pos += sp.second;
+        const size_t lo = std::max(s0, a), hi = std::min(pos, a + len);
+        if (lo >= hi) {
+            if (s0 >= a + len) break;
+            continue;
+        }
+        const off_t fo = (off_t)(sp.first + (lo - s0));
+        char *b = buf + (lo - a);
+        const size_t want = hi - lo;
+        size_t done = 0;
+        while (done < want) {
+            ssize_t r = write ? pwrite(fd, b + done, want - done, fo + (off_t)done)
+                              : pread(fd, b + done, want - done, fo + (off_t)done);
+            if (r <= 0) break;
+            done += (size_t)r;
+        }
+        if (done != want) {
+            *err = (write ? "short write to " : "short read from ") + x.path;
+            ok = false;
+            break;
+        }
+    }
+    close(fd);
+    return ok;
+}
 
 bool parse_u64_list(const std::string &s, char sep, std::vector<uint64_t> *out) {
     out->clear();
@@ -757,7 +828,7 @@ int phx_pod_create(phx_pod *out, size_t arena_bytes, int nstreams) {
         delete p;
         return rc;
     }
-    for (int i = 0; i <= nstreams; ++i) {
+    for (int i = 0; i < nstreams + 2; ++i) {
         hipStream_t s;
         hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
         if (e != hipSuccess) {
@@ -766,10 +837,14 @@ int phx_pod_create(phx_pod *out, size_t arena_bytes, int nstreams) {
         }
         if (i == nstreams)
             p->copy_stream = s;
+        else if (i == nstreams + 1)
+            p->store_stream = s;
         else
             p->streams.push_back(s);
     }
-    p->io = new IoPool(4);
+    p->io = new IoPool(io_threads());
+    p->stage_bytes = env_clamped("PHX_POD_STAGE_MIB", 8, 1, 1024) << 20;
+    p->stage_chunks = env_clamped("PHX_POD_STAGE_CHUNKS", 32, 2, 256);
     *out = p;
     return PHX_OK;
 }
@@ -779,7 +854,8 @@ int phx_pod_destroy(phx_pod p) {
     delete p->io;
     for (auto s : p->streams) (void)hipStreamDestroy(s);
     if (p->copy_stream) (void)hipStreamDestroy(p->copy_stream);
-    for (void *h : p->pinned_all) (void)hipHostFree(h);
+    if (p->store_stream) (void)hipStreamDestroy(p->store_stream);
+    for (void *h : p->stage_all) (void)hipHostFree(h);
     phx_arena_destroy(p->arena);
     delete p;
     return PHX_OK;
@@ -914,6 +990,22 @@ static int run_instrs(phx_pod p, std::vector<Instr> &ins, uint64_t stats[8]) {
         }
     uint64_t st[8] = {0};
     const uint64_t t0 = now_ns();
+    // compute_ns is the time at least one COMPUTE was running: leaves on the
+    // pod's streams may overlap each other, so their intervals, timed from an
+    // origin event recorded before any of them, are merged at the end rather
+    // than their durations summed.
+    struct Origin {
+        hipEvent_t ev = nullptr;
+        ~Origin() {
+            if (ev) (void)hipEventDestroy(ev);
+        }
+    } origin;
+    if (hipEventCreate(&origin.ev) != hipSuccess ||
+        hipEventRecord(origin.ev, p->streams[0]) != hipSuccess) {
+        if (origin.ev) (void)hipEventDestroy(origin.ev);
+        origin.ev = nullptr;
+    }
+    std::vector<std::pair<float, float>> busy;  // kernel [start, end) in ms after origin
 
     std::set<size_t> ready;  // ordered by segment position
     for (size_t i = 0; i < n; ++i)
@@ -930,19 +1022,82 @@ static int run_instrs(phx_pod p, std::vector<Instr> &ins, uint64_t stats[8]) {
         for (size_t d : dependents[i])
             if (--pending[d] == 0) ready.insert(d);
     };
-    auto get_pinned = [&](size_t bytes) -> void * {
-        auto it = p->pinned_free.find(bytes);
-        if (it != p->pinned_free.end()) {
-            void *h = it->second;
-            p->pinned_free.erase(it);
-            return h;
+    // LOADs and STOREs in progress, and those with chunks not yet staged
+    // (first issued, first served, so the earliest transfer finishes first)
+    std::map<size_t, Xfer> xfers;
+    std::deque<size_t> xq;
+    auto take_stage = [&](void **h) -> int {
+        *h = nullptr;
+        if (!p->stage_free.empty()) {
+            *h = p->stage_free.back();
+            p->stage_free.pop_back();
+        } else if (p->stage_all.size() < p->stage_chunks) {
+            if (hipHostMalloc(h, p->stage_bytes, hipHostMallocDefault) != hipSuccess) {
+                *h = nullptr;
+                if (p->stage_all.empty())  // none will ever come back
+                    return set_error(PHX_E_IO, "pinned staging of %zu bytes failed",
+                                     p->stage_bytes);
+            } else {
+                p->stage_all.push_back(*h);
+            }
         }
-        void *h = nullptr;
-        if (hipHostMalloc(&h, bytes, hipHostMallocDefault) != hipSuccess) return nullptr;
-        p->pinned_all.push_back(h);
-        return h;
+        return PHX_OK;
     };
-    auto put_pinned = [&](void *h, size_t bytes) { p->pinned_free.insert({bytes, h}); };
+    auto chunk_range = [&](const Xfer &x, size_t c, size_t *a, size_t *len) {
+        *a = c * p->stage_bytes;
+        *len = std::min(p->stage_bytes, x.bytes - *a);
+    };
+    // stages every chunk that a free staging buffer allows: a LOAD chunk goes
+    // to a worker for its file read, a STORE chunk to the D2H copy stream
+    auto pump = [&]() -> int {
+        while (!xq.empty()) {
+            const size_t idx = xq.front();
+            Xfer &x = xfers.at(idx);
+            if (x.next == x.nchunks) {
+                xq.pop_front();
+                continue;
+            }
+            void *h;
+            if (int rc = take_stage(&h)) return rc;
+            if (!h) return PHX_OK;  // all chunks busy: wait for one to come back
+            const size_t c = x.next++;
+            size_t a, len;
+            chunk_range(x, c, &a, &len);
+            if (x.load) {
+                const Xfer *xp = &x;  // map nodes stay put until the transfer ends
+                io_pending++;
+                p->io->submit([&, idx, c, h, a, len, xp]() {
+                    const uint64_t s0 = now_ns();
+                    IoDone d{idx, c, true, "", 0, h};
+                    d.ok = chunk_io(*xp, false, (char *)h, a, len, &d.err);
+                    d.ns = now_ns() - s0;
+                    std::lock_guard<std::mutex> l(io_mu);
+                    io_done.push_back(d);
+                });
+            } else {
+                Inflight f{Inflight::D2H, idx};
+                f.chunk = c;
+                f.staging = h;
+                inflight.push_back(f);  // the drain accounts for the chunk from here on
+                Inflight &g = inflight.back();
+                hipError_t e = hipMemcpyAsync(h, (void *)(uintptr_t)(x.dev + a), len,
+                                              hipMemcpyDeviceToHost, p->store_stream);
+                if (e == hipSuccess) e = hipEventCreateWithFlags(&g.done, hipEventDisableTiming);
+                if (e == hipSuccess) e = hipEventRecord(g.done, p->store_stream);
+                if (e != hipSuccess) return hip_error(e, "STORE hipMemcpyAsync");
+            }
+        }
+        return PHX_OK;
+    };
+    // a transfer's chunk arrived (LOAD: on the device; STORE: in the file)
+    auto chunk_landed = [&](size_t idx, void *h) {
+        p->stage_free.push_back(h);
+        Xfer &x = xfers.at(idx);
+        if (++x.landed < x.nchunks) return;
+        st[x.load ? 1 : 3]++;
+        xfers.erase(idx);
+        complete(idx);
+    };
     auto tile_of = [&](uint64_t id, TileBuf **out) -> int {
         auto it = p->tiles.find(id);
         if (it == p->tiles.end())
@@ -1009,78 +1164,35 @@ static int run_instrs(phx_pod p, std::vector<Instr> &ins, uint64_t stats[8]) {
             parked_alloc.clear();
             return PHX_OK;
         }
-        case OpKind::Load: {
-            TileBuf *tb;
-            if (int rc = tile_of(I.tile, &tb)) return rc;
-            auto tit = p->tensors.find(I.tensor);
-            if (tit == p->tensors.end())
-                return set_error(PHX_E_SEGMENT, "LOAD of unregistered tensor %u", I.tensor);
-            if (int rc = region_ok(I, *tb, tit->second)) return rc;
-            const size_t bytes = tb->elems * 4;
-            void *h = get_pinned(bytes);
-            if (!h) return set_error(PHX_E_IO, "pinned staging of %zu bytes failed", bytes);
-            const TensorInfo ti = tit->second;
-            const Region rg = I.region;
-            io_pending++;
-            p->io->submit([&, i, h, ti, rg]() {
-                uint64_t s0 = now_ns();
-                IoDone d{i, true, "", 0, nullptr, 0};
-                std::vector<std::pair<uint64_t, size_t>> spans;
-                int fd = open(ti.path.c_str(), O_RDONLY);
-                if (fd < 0 || !byte_spans(ti.shape, rg, &spans)) {
-                    d.ok = false;
-                    d.err = "cannot open/read " + ti.path;
-                } else {
-                    char *dst = (char *)h;
-                    for (auto &sp : spans) {
-                        size_t want = sp.second * 4, got = 0;
-                        while (got < want) {
-                            ssize_t r = pread(fd, dst + got, want - got, (off_t)(sp.first + got));
-                            if (r <= 0) break;
-                            got += (size_t)r;
-                        }
-                        if (got != want) {
-                            d.ok = false;
-                            d.err = "short read from " + ti.path;
-                            break;
-                        }
-                        dst += want;
-                    }
-                }
-                if (fd >= 0) close(fd);
-                d.ns = now_ns() - s0;
-                std::lock_guard<std::mutex> l(io_mu);
-                io_done.push_back(d);
-            });
-            Inflight f{Inflight::H2D, i};
-            f.staging = h;
-            f.staging_bytes = bytes;
-            inflight.push_back(f);  // copy is enqueued once the read lands
-            inflight.back().done = nullptr;
-            return PHX_OK;
-        }
+        case OpKind::Load:
         case OpKind::Store: {
+            const bool load = I.kind == OpKind::Load;
             TileBuf *tb;
             if (int rc = tile_of(I.tile, &tb)) return rc;
             auto tit = p->tensors.find(I.tensor);
             if (tit == p->tensors.end())
-                return set_error(PHX_E_SEGMENT, "STORE to unregistered tensor %u", I.tensor);
+                return set_error(PHX_E_SEGMENT, load ? "LOAD of unregistered tensor %u"
+                                                     : "STORE to unregistered tensor %u",
+                                 I.tensor);
             if (int rc = region_ok(I, *tb, tit->second)) return rc;
-            const size_t bytes = tb->elems * 4;
-            void *h = get_pinned(bytes);
-            if (!h) return set_error(PHX_E_IO, "pinned staging of %zu bytes failed", bytes);
-            Inflight f{Inflight::D2H, i};
-            f.staging = h;
-            f.staging_bytes = bytes;
-            hipError_t e = hipMemcpyAsync(h, (void *)(uintptr_t)tb->addr, bytes,
-                                          hipMemcpyDeviceToHost, p->copy_stream);
-            if (e != hipSuccess) return hip_error(e, "STORE hipMemcpyAsync");
-            if ((e = hipEventCreateWithFlags(&f.done, hipEventDisableTiming)) != hipSuccess)
-                return hip_error(e, "hipEventCreate");
-            if ((e = hipEventRecord(f.done, p->copy_stream)) != hipSuccess)
-                return hip_error(e, "hipEventRecord");
-            inflight.push_back(f);
-            return PHX_OK;
+            Xfer x;
+            x.load = load;
+            x.dev = tb->addr;
+            x.bytes = tb->elems * 4;
+            x.nchunks = (x.bytes + p->stage_bytes - 1) / p->stage_bytes;
+            x.path = tit->second.path;
+            if (!byte_spans(tit->second.shape, I.region, &x.spans))
+                return set_error(PHX_E_IO, "cannot %s %s", load ? "open/read" : "open/write",
+                                 x.path.c_str());
+            for (auto &sp : x.spans) sp.second *= 4;
+            if (x.nchunks == 0) {
+                st[load ? 1 : 3]++;
+                complete(i);
+                return PHX_OK;
+            }
+            xfers.emplace(i, std::move(x));
+            xq.push_back(i);
+            return pump();
         }
         case OpKind::Compute: {
             auto kit = p->kernels.find(I.kernel);
@@ -1171,6 +1283,8 @@ static int run_instrs(phx_pod p, std::vector<Instr> &ins, uint64_t stats[8]) {
             progress = true;
         }
         if (err) break;
+        // chunks of queued transfers that staging buffers freed since
+        if ((err = pump())) break;
         // file reads/writes that finished
         std::vector<IoDone> done;
         {
@@ -1184,29 +1298,26 @@ static int run_instrs(phx_pod p, std::vector<Instr> &ins, uint64_t stats[8]) {
             st[7] += d.ns;
             progress = true;
             if (err || !d.ok) {
-                if (d.staging) put_pinned(d.staging, d.bytes);  // STORE: the write is over
+                p->stage_free.push_back(d.staging);
                 if (!err) err = set_error(PHX_E_IO, "%s", d.err.c_str());
                 continue;
             }
-            Instr &I = ins[d.idx];
-            if (I.kind == OpKind::Load) {
-                for (auto &f : inflight)
-                    if (f.idx == d.idx && f.stage == Inflight::H2D && !f.done) {
-                        TileBuf *tb;
-                        if ((err = tile_of(I.tile, &tb))) break;
-                        hipError_t e = hipMemcpyAsync((void *)(uintptr_t)tb->addr, f.staging,
-                                                      f.staging_bytes, hipMemcpyHostToDevice,
-                                                      p->copy_stream);
-                        if (e == hipSuccess) e = hipEventCreateWithFlags(&f.done, hipEventDisableTiming);
-                        if (e == hipSuccess) e = hipEventRecord(f.done, p->copy_stream);
-                        if (e != hipSuccess) err = hip_error(e, "LOAD hipMemcpyAsync");
-                        break;
-                    }
-                if (err) continue;
-            } else {  // STORE finished writing the file
-                put_pinned(d.staging, d.bytes);
-                st[3]++;
-                complete(d.idx);
+            Xfer &x = xfers.at(d.idx);
+            if (x.load) {  // chunk read from the file: copy it to the tile
+                size_t a, len;
+                chunk_range(x, d.chunk, &a, &len);
+                Inflight f{Inflight::H2D, d.idx};
+                f.chunk = d.chunk;
+                f.staging = d.staging;
+                inflight.push_back(f);
+                Inflight &g = inflight.back();
+                hipError_t e = hipMemcpyAsync((void *)(uintptr_t)(x.dev + a), d.staging, len,
+                                              hipMemcpyHostToDevice, p->copy_stream);
+                if (e == hipSuccess) e = hipEventCreateWithFlags(&g.done, hipEventDisableTiming);
+                if (e == hipSuccess) e = hipEventRecord(g.done, p->copy_stream);
+                if (e != hipSuccess) err = hip_error(e, "LOAD hipMemcpyAsync");
+            } else {  // chunk written to the file
+                chunk_landed(d.idx, d.staging);
             }
         }
         if (err) break;
@@ -1227,52 +1338,29 @@ static int run_instrs(phx_pod p, std::vector<Instr> &ins, uint64_t stats[8]) {
                 break;
             }
             progress = true;
-            Instr &I = ins[f.idx];
             if (f.stage == Inflight::Kernel) {
-                float ms = 0;
-                if (hipEventElapsedTime(&ms, f.start, f.done) == hipSuccess)
-                    st[5] += (uint64_t)(ms * 1e6);
+                float a = 0, b = 0;
+                if (origin.ev && hipEventElapsedTime(&a, origin.ev, f.start) == hipSuccess &&
+                    hipEventElapsedTime(&b, origin.ev, f.done) == hipSuccess)
+                    busy.push_back({a, b});
+                else if (hipEventElapsedTime(&b, f.start, f.done) == hipSuccess)
+                    st[5] += (uint64_t)(b * 1e6);  // no origin: the plain duration
                 (void)hipEventDestroy(f.start);
                 st[2]++;
                 complete(f.idx);
             } else if (f.stage == Inflight::H2D) {
-                put_pinned(f.staging, f.staging_bytes);
-                st[1]++;
-                complete(f.idx);
-            } else {  // D2H landed: write the file on the pool
-                auto tit = p->tensors.find(I.tensor);
-                const TensorInfo ti = tit->second;
-                const Region rg = I.region;
+                chunk_landed(f.idx, f.staging);
+            } else {  // D2H landed: write the chunk to the file on the pool
+                const Xfer *xp = &xfers.at(f.idx);
+                const size_t idx = f.idx, c = f.chunk;
                 void *h = f.staging;
-                size_t bytes = f.staging_bytes;
-                size_t idx = f.idx;
+                size_t a, len;
+                chunk_range(*xp, c, &a, &len);
                 io_pending++;
-                p->io->submit([&, idx, h, bytes, ti, rg]() {
-                    uint64_t s0 = now_ns();
-                    IoDone d{idx, true, "", 0, h, bytes};
-                    std::vector<std::pair<uint64_t, size_t>> spans;
-                    int fd = open(ti.path.c_str(), O_RDWR | O_CREAT, 0644);
-                    if (fd < 0 || !byte_spans(ti.shape, rg, &spans)) {
-                        d.ok = false;
-                        d.err = "cannot open/write " + ti.path;
-                    } else {
-                        const char *src = (const char *)h;
-                        for (auto &sp : spans) {
-                            size_t want = sp.second * 4, put = 0;
-                            while (put < want) {
-                                ssize_t w = pwrite(fd, src + put, want - put, (off_t)(sp.first + put));
-                                if (w <= 0) break;
-                                put += (size_t)w;
-                            }
-                            if (put != want) {
-                                d.ok = false;
-                                d.err = "short write to " + ti.path;
-                                break;
-                            }
-                            src += want;
-                        }
-                    }
-                    if (fd >= 0) close(fd);
+                p->io->submit([&, idx, c, h, a, len, xp]() {
+                    const uint64_t s0 = now_ns();
+                    IoDone d{idx, c, true, "", 0, h};
+                    d.ok = chunk_io(*xp, true, (char *)h, a, len, &d.err);
                     d.ns = now_ns() - s0;
                     std::lock_guard<std::mutex> l(io_mu);
                     io_done.push_back(d);
@@ -1301,11 +1389,10 @@ static int run_instrs(phx_pod p, std::vector<Instr> &ins, uint64_t stats[8]) {
     if (err) {
         for (auto s : p->streams) (void)hipStreamSynchronize(s);
         (void)hipStreamSynchronize(p->copy_stream);
+        (void)hipStreamSynchronize(p->store_stream);
         for (;;) {
             {
                 std::lock_guard<std::mutex> l(io_mu);
-                for (auto &d : io_done)
-                    if (d.staging) put_pinned(d.staging, d.bytes);
                 io_pending -= io_done.size();
                 io_done.clear();
             }
@@ -1315,8 +1402,8 @@ static int run_instrs(phx_pod p, std::vector<Instr> &ins, uint64_t stats[8]) {
         for (auto &f : inflight) {
             if (f.start) (void)hipEventDestroy(f.start);
             if (f.done) (void)hipEventDestroy(f.done);
-            if (f.staging) put_pinned(f.staging, f.staging_bytes);
         }
+        p->stage_free = p->stage_all;  // nothing is in flight any more
         for (uint64_t id : allocated_here) {
             auto it = p->tiles.find(id);
             if (it == p->tiles.end()) continue;
@@ -1324,6 +1411,14 @@ static int run_instrs(phx_pod p, std::vector<Instr> &ins, uint64_t stats[8]) {
             p->tiles.erase(it);
         }
         return err;
+    }
+    std::sort(busy.begin(), busy.end());
+    for (size_t a = 0; a < busy.size();) {  // union of the kernel intervals
+        float lo = busy[a].first, hi = busy[a].second;
+        size_t b = a + 1;
+        for (; b < busy.size() && busy[b].first <= hi; ++b) hi = std::max(hi, busy[b].second);
+        st[5] += (uint64_t)((double)(hi - lo) * 1e6);
+        a = b;
     }
     st[6] = now_ns() - t0;
     if (stats) memcpy(stats, st, sizeof st);

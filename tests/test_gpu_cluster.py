@@ -49,7 +49,7 @@ def test_chain_matches_leaf_replay(px_gpu, tmp_path):
 
 def test_arena_exhausted_is_reported(px_gpu, tmp_path):
     import phobos_amd as px
-    with pytest.raises(px.PhxError) as e:
+    with pytest.raises(cl.PhxError) as e:
         cl.run_matmul_job(str(tmp_path), 512, 512, 512, 256, 256, 256, 0.125, 1.5,
                           arena_bytes=1 << 16)
     assert e.value.code == px.PHX_E_EXHAUSTED
@@ -58,10 +58,10 @@ def test_arena_exhausted_is_reported(px_gpu, tmp_path):
 def test_malformed_segment_rejected(px_gpu):
     import phobos_amd as px
     pod = cl.Pod(1 << 20, 2)
-    with pytest.raises(px.PhxError) as e:
+    with pytest.raises(cl.PhxError) as e:
         pod.run("1 - ALLOC 0x1 16x16 f32\n2 7 FREE 0x1 0\n")
     assert e.value.code == 1006
-    with pytest.raises(px.PhxError):
+    with pytest.raises(cl.PhxError):
         pod.run("1 - BOGUS 0x1\n")
     pod.close()
 
@@ -301,7 +301,7 @@ def test_io_errors_return_promptly_and_release_the_segment(px_gpu, tmp_path):
     bad = [f"{i} - ALLOC {100 + i} {n} f32" for i in range(1, 9)]
     bad += [f"{10 + i} {i} LOAD {100 + i} 0 0 {n}" for i in range(1, 9)]
     t0 = time.monotonic()
-    with pytest.raises(px.PhxError) as e:
+    with pytest.raises(cl.PhxError) as e:
         pod.run("\n".join(bad) + "\n")
     assert time.monotonic() - t0 < 10
     assert e.value.code == 1005 and "missing.bin" in str(e.value)
@@ -335,4 +335,51 @@ def test_flat_region_over_a_2d_tensor(px_gpu, tmp_path):
     got = np.fromfile(dst, np.float32)
     want = np.concatenate([x[half:], x[half:]])
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    pod.close()
+
+
+@pytest.mark.gpu
+def test_multi_chunk_transfers(px_gpu, tmp_path):
+    # Tiles larger than one staging chunk (8 MiB) move chunk by chunk: a
+    # 2900 x 2400 region (27.8 MB, rows of 9600 bytes straddling chunk
+    # boundaries) and a flat 2500001-element region (two chunks and a ragged
+    # tail) go file -> device -> file unchanged.  The pod runs the segment
+    # twice, then a segment whose LOAD fails, then the good one again, so
+    # staging buffers come back after success and after failure alike.
+    R, C = 3000, 2500
+    src, dst, fsrc, fdst = (str(tmp_path / n) for n in ("s.bin", "d.bin", "fs.bin", "fd.bin"))
+    x = oracle.lcg_f32(9, R * C)
+    x.tofile(src)
+    x.tofile(fsrc)
+    pod = cl.Pod(64 << 20, nstreams=2)
+    pod.set_tensor(0, "file://" + src, (R, C))
+    pod.set_tensor(1, "file://" + dst, (R, C))
+    pod.set_tensor(2, "file://" + fsrc, (R * C,))
+    pod.set_tensor(3, "file://" + fdst, (R * C,))
+    pod.set_tensor(4, "file://" + str(tmp_path / "missing.bin"), (R, C))
+    n = 2500001
+    seg = "\n".join([
+        "1 - ALLOC 301 2900x2400 f32", f"2 - ALLOC 302 {n} f32",
+        "3 1 LOAD 301 0 7,13 2900,2400", f"4 2 LOAD 302 2 123 {n}",
+        "5 3 STORE 301 1 50,61 2900,2400", f"6 4 STORE 302 3 1000 {n}",
+        "7 5 FREE 301 0", "8 6 FREE 302 0"]) + "\n"
+    bad = seg.replace("LOAD 301 0 7,13", "LOAD 301 4 7,13")
+    xm = x.reshape(R, C)
+    for run in ("good", "good", "bad", "good"):
+        np.zeros(R * C, np.float32).tofile(dst)
+        np.zeros(R * C, np.float32).tofile(fdst)
+        if run == "bad":
+            with pytest.raises(cl.PhxError):
+                pod.run(bad)
+            continue
+        st = pod.run(seg)
+        assert st["load"] == 2 and st["store"] == 2
+        got = np.fromfile(dst, np.float32).reshape(R, C)
+        want = np.zeros((R, C), np.float32)
+        want[50:2950, 61:2461] = xm[7:2907, 13:2413]
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+        gf = np.fromfile(fdst, np.float32)
+        wf = np.zeros(R * C, np.float32)
+        wf[1000:1000 + n] = x[123:123 + n]
+        assert np.array_equal(gf.view(np.uint32), wf.view(np.uint32))
     pod.close()
