@@ -438,7 +438,7 @@ template <bool PART>
 __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp, T *O,
                                             int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo,
                                             uint32_t Nq, uint32_t Nk, uint32_t q0, float scale,
-                                            char *st0, char *st1, char *st2, char *st3,
+                                            char *st,
                                             float *pacc, float *pml) {
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -446,7 +446,9 @@ __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp
     const uint32_t qw = q0 + wave * WQ;  // first query of this wave
     const float c2 = softmax_c2(scale);
     const uint32_t nkb = (Nk + BC - 1) / BC;
-    char *const S[NSTAGE] = {st0, st1, st2, st3};
+    char *S[NSTAGE];  // stage b % NSTAGE holds key block b
+#pragma unroll
+    for (int k = 0; k < NSTAGE; ++k) S[k] = st + k * STAGE_BYTES;
 
     // per-lane source offsets of the LDS copies (see dma_block): the K
     // swizzle depends on bit 2 of the row, i.e. on the wave's parity
@@ -479,7 +481,7 @@ __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp
     // The full blocks run pipelined; a partial last block (Nk % 64 keys) follows.
     // Block 0 (the first step, whose scores are masked when Nk < 64) always runs.
     const uint32_t nfull = Nk / BC;
-    flash16_step<true>(fs, S[0], S[3], Kp, Vp, ldk, ldv, Nk, 0, c2, vk, vv, wave, lane);
+    flash16_step<true>(fs, S[0], S[NSTAGE - 1], Kp, Vp, ldk, ldv, Nk, 0, c2, vk, vv, wave, lane);
     uint32_t i = 1;
     for (; i + NSTAGE <= nfull; i += NSTAGE) {
         flash16_step<false>(fs, S[1], S[0], Kp, Vp, ldk, ldv, Nk, i, c2, vk, vv, wave, lane);
@@ -493,12 +495,9 @@ __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp
         flash16_step<false>(fs, S[2], S[1], Kp, Vp, ldk, ldv, Nk, i + 1, c2, vk, vv, wave, lane);
     if (i + 2 < nfull)
         flash16_step<false>(fs, S[3], S[2], Kp, Vp, ldk, ldv, Nk, i + 2, c2, vk, vv, wave, lane);
-    if (nfull > 0 && nfull < nkb) {  // wave-uniform; the stage is a constant in each case
+    if (nfull > 0 && nfull < nkb) {  // wave-uniform
         const uint32_t kv = Nk - nfull * BC;
-        if (nfull % 4 == 0) flash16_last(fs, S[0], kv, c2, lane);
-        else if (nfull % 4 == 1) flash16_last(fs, S[1], kv, c2, lane);
-        else if (nfull % 4 == 2) flash16_last(fs, S[2], kv, c2, lane);
-        else flash16_last(fs, S[3], kv, c2, lane);
+        flash16_last(fs, st + (nfull % NSTAGE) * STAGE_BYTES, kv, c2, lane);
     }
     // drain the copies of the blocks past the end before the LDS is reused
     PHX_WAIT_VMCNT(0);
@@ -746,11 +745,11 @@ __device__ __forceinline__ void flash_block(const T *Q, const T *Kp, const T *Vp
 // one array, so every stage address is a constant offset from one base
 #define FA_LDS_DECL __shared__ __attribute__((aligned(16))) char st[NSTAGE][STAGE_BYTES];
 #define FA_CALL(Qp, Kp, Vp, Op, ldq, ldk, ldv, ldo, Nq, Nk, q0) \
-    flash_block<false>(Qp, Kp, Vp, Op, ldq, ldk, ldv, ldo, Nq, Nk, q0, scale, st[0], st[1], \
-                       st[2], st[3], nullptr, nullptr)
+    flash_block<false>(Qp, Kp, Vp, Op, ldq, ldk, ldv, ldo, Nq, Nk, q0, scale, &st[0][0], nullptr, \
+                       nullptr)
 #define FA_CALL_PART(Qp, Kp, Vp, ldq, ldk, ldv, Nq, Nk, q0, pacc, pml)                    \
-    flash_block<true>(Qp, Kp, Vp, nullptr, ldq, ldk, ldv, 0, Nq, Nk, q0, scale, st[0], st[1], \
-                      st[2], st[3], pacc, pml)
+    flash_block<true>(Qp, Kp, Vp, nullptr, ldq, ldk, ldv, 0, Nq, Nk, q0, scale, &st[0][0], pacc, \
+                      pml)
 #else
 #define FA_QB BR
 #define FA_LDS_DECL __shared__ __attribute__((aligned(16))) char lds[2][2][TILE_BYTES];
