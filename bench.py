@@ -85,7 +85,10 @@ def parse():
                     help="run only one benchmark, as phobos-bench --bench NAME: one of "
                          + ", ".join(BENCHES))
     ap.add_argument("--autotune", default=None, metavar="SPEC",
-                    help="phobos-bench's tile pins; refused here: these kernels have one tiling each")
+                    help="pin the launch plan instead of searching it, as phobos-bench's "
+                         "--autotune pins its tile dims (needs --bench): \"splits=N variant=V\"")
+    ap.add_argument("--no-autotune", action="store_true",
+                    help="skip the launch-plan search and use the runtime's built-in plans")
     ap.add_argument("--shapes", action="store_true",
                     help="only time the non-BASELINE shapes that run split (GEMMs at 512^3 and "
                          "1024^3, one-head flash at 4096 queries, through the .ph entries) and exit")
@@ -95,11 +98,23 @@ def parse():
         if args.bench not in BENCHES:
             ap.error(f"unknown --bench '{args.bench}'; available: {', '.join(BENCHES)}")
         args.kernels = args.bench
+    args.pins = {}
     if args.autotune is not None:
-        ap.error("--autotune pins the reference's TILE_M/TILE_N/TILE_K/BR/BC search; the MI355X "
-                 "kernels have one tiling each (GEMM 256x256, K step 32; flash 128 or 256 "
-                 "queries x 64 keys) and no search to pin; problems too small to fill the GPU "
-                 "are split over K or over the keys instead (phx_split_plan)")
+        # phobos-bench/src/main.rs:68-72, 118-119, 149-160: NAME=VALUE pins, one benchmark
+        if args.bench is None:
+            ap.error("--autotune pins are kernel-specific; pass --bench to pick one")
+        for tok in args.autotune.replace(",", " ").split():
+            name, eq, val = tok.partition("=")
+            if not eq:
+                ap.error(f"bad autotune pin '{tok}', expected NAME=VALUE")
+            if name not in ("splits", "variant"):
+                # autotune.rs:42-51
+                ap.error(f"autotune pin '{name}' is not a search dim of this kernel "
+                         "(dims: splits, variant)")
+            try:
+                args.pins[name] = int(val)
+            except ValueError:
+                ap.error(f"autotune pin '{name}' has a non-integer value '{val}'")
     return args
 
 
@@ -198,11 +213,22 @@ def setup(px, stream, wanted):
     return ks
 
 
-def shapes_leg(px, stream, reps=20):
+def shapes_leg(px, stream, reps=20, tune=True):
     """Time the shapes that run split (phx_split_plan): each GEMM at 512^3 and
     1024^3, and the one-head flash .ph entry (main.rs:334-371) at 4096 x 4096.
-    Inputs as in the BASELINE configs, average of `reps` launches after 3."""
+    Inputs as in the BASELINE configs, average of `reps` launches after 3,
+    under the built-in plan; with tune, also the autotuner's winner and its
+    fastest launch (the pin is removed again afterwards)."""
+    from phobos_amd import autotune
     out = []
+
+    def tuned(kid, dims, fn):
+        if not tune:
+            return None
+        r = fn()
+        px.plan_pin(kid, dims, None)
+        return {"plan": list(r["winner"]), "us": round(r["us"], 2)}
+
     ev0, ev1 = px.Event(), px.Event()
 
     def timed(fn):
@@ -230,7 +256,9 @@ def shapes_leg(px, stream, reps=20):
             sp, ws = px.split_plan(kid, [n, n, n])
             out.append({"kernel": name, "shape": [n, n, n], "splits": sp, "workspace_bytes": ws,
                         "us": round(ms * 1e3, 2),
-                        "tflops": round((2 * n ** 3 + n * n) / (ms / 1e3) / 1e12, 2)})
+                        "tflops": round((2 * n ** 3 + n * n) / (ms / 1e3) / 1e12, 2),
+                        "autotuned": tuned(kid, [n, n, n],
+                                           lambda: autotune.tune_gemm(stream, kid, n, n, n))})
     S, D = 4096, 64
     for name, kid, esz in (("flash_fp32", px.FLASH_FP32, 4), ("flash_fp16", px.FLASH_FP16, 2)):
         ts = [px.normal_f32(sd, S * D) for sd in (1, 2, 3)]
@@ -242,7 +270,45 @@ def shapes_leg(px, stream, reps=20):
         sp, ws = px.split_plan(kid, [S, S, D])
         out.append({"kernel": name + " (one head)", "shape": [S, S, D], "splits": sp,
                     "workspace_bytes": ws, "us": round(ms * 1e3, 2),
-                    "tflops": round(4 * S * S * D / (ms / 1e3) / 1e12, 2)})
+                    "tflops": round(4 * S * S * D / (ms / 1e3) / 1e12, 2),
+                    "autotuned": tuned(kid, [S, S, D],
+                                       lambda: autotune.tune_flash(stream, kid, 1, S, S))})
+    return out
+
+
+def autotune_leg(px, stream, wanted, pins):
+    """The launch-plan search of every benchmark kernel at its BASELINE
+    shape and arguments, before the timed steps, as phobos-bench tunes each
+    benchmark before it times it (main.rs:461-530); the winners stay pinned
+    for the timed launches.  With pins (--autotune, one benchmark) the plan is
+    pinned without a search."""
+    from phobos_amd import autotune
+    N = 4096
+    jobs = {"gemm_fp32": ("gemm", px.GEMM_FP32, (N, N, N), dict(alpha=0.125, beta=1.5)),
+            "gemm_fp16tc_fp32acc": ("gemm", px.GEMM_FP16TC_FP32ACC, (N, N, N), {}),
+            "gemm_fp16": ("gemm", px.GEMM_FP16, (N, N, N), {}),
+            "flash_fp32": ("flash", px.FLASH_FP32_BH, (64, N, N), {}),
+            "flash_fp16": ("flash", px.FLASH_FP16_BH, (64, N, N), {})}
+    out = {}
+    for name in wanted:
+        if name not in jobs:
+            continue  # saxpy has no plan choices
+        kind, kid, dims, kw = jobs[name]
+        pdims = list(dims) + ([64] if kind == "flash" else [])
+        if pins:
+            px.plan_pin(kid, pdims, pins.get("splits", 1), pins.get("variant", 0))
+            out[name] = {"pinned": list(px.plan_get(kid, pdims))}
+            continue
+        t0 = time.perf_counter()
+        if kind == "gemm":
+            r = autotune.tune_gemm(stream, kid, *dims, **kw)
+        else:
+            r = autotune.tune_flash(stream, kid, *dims)
+        out[name] = {"winner": list(r["winner"]), "us": round(r["us"], 2),
+                     "finalists": [[list(f["plan"]), round(f["us"], 2)] for f in r["stage2"]],
+                     "plans_tried": len(r["stage1"]), "s": round(time.perf_counter() - t0, 2)}
+        log(f"autotune {name}: winner (splits, variant) = {r['winner']}, {r['us']:.1f} us; "
+            f"finalists {out[name]['finalists']}")
     return out
 
 
@@ -454,16 +520,19 @@ def main():
     info = px.device_info()
     log(f"device: {info}")
     if args.shapes:
-        res = shapes_leg(px, px.Stream())
+        res = shapes_leg(px, px.Stream(), tune=not args.no_autotune)
         for r in res:
             log(f"{r['kernel']:28s} {str(r['shape']):18s} splits {r['splits']:2d}  "
-                f"{r['us']:8.2f} us  {r['tflops']:8.2f} TFLOP/s")
+                f"{r['us']:8.2f} us  {r['tflops']:8.2f} TFLOP/s  autotuned {r['autotuned']}")
         print(json.dumps({"shapes": res, "device": info}), flush=True)
         return
     all_names = ["saxpy_fp32", "gemm_fp32", "gemm_fp16tc_fp32acc", "gemm_fp16", "flash_fp32",
                  "flash_fp16"]
     wanted = all_names if args.kernels == "all" else args.kernels.split(",")
     stream = px.Stream()
+    tuned = None
+    if not args.no_autotune and not args.hold:
+        tuned = autotune_leg(px, stream, wanted, args.pins)
     ks = setup(px, stream, wanted)
     if args.hold > 0:
         t0, n = time.perf_counter(), 0
@@ -568,6 +637,7 @@ def main():
         "cpu_baseline": cpu,
         "cpu_legs": cpu_more,
         "kernels": kern,
+        "autotune": tuned,
         "matmul_cluster": cluster_res,
         "device": info,
     }

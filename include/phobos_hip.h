@@ -154,6 +154,32 @@ int phx_check_shape(phx_kernel k, const int64_t *dims, int ndims);
 int phx_split_plan(phx_kernel k, const int64_t *dims, int ndims, int *splits,
                    size_t *workspace_bytes);
 
+/* A launch plan of a built-in kernel at one problem shape: the dims the
+ * autotuner searches (phobos_amd.autotune).  The reference's autotuner picks
+ * compile-time tile sizes by timing every choice
+ * (phobos-bench/src/autotune.rs:98-192; the @autotune dims of the .ph
+ * kernels); here each kernel has one tile shape and these are its choices:
+ *   splits   K chunks (gemm_fp32, gemm_fp16tc_fp32acc, gemm_fp16) or key
+ *            chunks (flash), 1 .. 16, 1 for none;
+ *   variant  gemm_fp16tc_fp32acc on whole 256 x 256 tiles: 0 the eight-wave
+ *            kernel, 1 the one-wave kernel; 0 for every other kernel.
+ * A launch uses the plan pinned for its kernel and dims, else the built-in
+ * rule.  The PHX_GEMM_SPLIT, PHX_FLASH_SPLIT and PHX_GEMM_W8 environment
+ * variables, which force a plan for measurement, take precedence over both. */
+typedef struct {
+    int32_t splits;
+    int32_t variant;
+} phx_plan;
+/* The plan a launch of k over dims (as phx_grid_for) would use now. */
+int phx_plan_get(phx_kernel k, const int64_t *dims, int ndims, phx_plan *plan);
+/* Pins plan for k at dims (plan NULL removes the pin).  The one-head and
+ * batched flash kernels of a precision share pins, the one-head dims meaning
+ * one head.  PHX_E_INVALID for a kernel without choices, splits outside
+ * 1 .. 16 or a variant the kernel lacks. */
+int phx_plan_pin(phx_kernel k, const int64_t *dims, int ndims, const phx_plan *plan);
+/* Removes every pin. */
+int phx_plan_unpin_all(void);
+
 /* --- Pod COMPUTE marshalling (engine.rs:582-630) ---
  * Each tile argument becomes the exploded memref
  *   (ptr, ptr, offset=0, sizes[rank], strides[rank] row-major)

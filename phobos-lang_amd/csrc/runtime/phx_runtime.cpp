@@ -335,6 +335,47 @@ static int builtin_dims(phx_kernel k, void **args, int64_t *d, int *nd, Desc *t)
     }
 }
 
+// Plans pinned by phx_plan_pin, keyed by kernel family and problem dims:
+// GEMMs by (kernel, M, N, K), flash by (precision, heads, Nq, Nk).
+namespace {
+struct PlanKey {
+    int fam;
+    int64_t a, b, c;
+    bool operator==(const PlanKey &o) const {
+        return fam == o.fam && a == o.a && b == o.b && c == o.c;
+    }
+};
+struct PlanKeyHash {
+    size_t operator()(const PlanKey &k) const {
+        size_t h = (size_t)k.fam;
+        for (int64_t v : {k.a, k.b, k.c}) h = h * 1000003u ^ (size_t)v;
+        return h;
+    }
+};
+std::mutex g_plan_mu;
+std::unordered_map<PlanKey, phx_plan, PlanKeyHash> g_plans;
+
+bool pinned_plan(const PlanKey &key, phx_plan *out) {
+    std::lock_guard<std::mutex> lock(g_plan_mu);
+    auto it = g_plans.find(key);
+    if (it == g_plans.end()) return false;
+    *out = it->second;
+    return true;
+}
+bool is_gemm(phx_kernel k) {
+    return k == PHX_GEMM_FP32 || k == PHX_GEMM_FP16TC_FP32ACC || k == PHX_GEMM_FP16;
+}
+bool is_flash(phx_kernel k) {
+    return k == PHX_FLASH_FP16 || k == PHX_FLASH_FP32 || k == PHX_FLASH_FP16_BH ||
+           k == PHX_FLASH_FP32_BH;
+}
+PlanKey gemm_key(phx_kernel k, int64_t M, int64_t N, int64_t K) { return {(int)k, M, N, K}; }
+PlanKey flash_key(phx_kernel k, int64_t BH, int64_t Nq, int64_t Nk) {
+    const bool f16 = k == PHX_FLASH_FP16 || k == PHX_FLASH_FP16_BH;
+    return {f16 ? -1 : -2, BH, Nq, Nk};
+}
+}  // namespace
+
 // How many K chunks a GEMM is split into (1: no split).  A GEMM whose
 // 256 x 256 output tiles cannot fill half of the 256 CUs gets enough chunks
 // to give every CU a workgroup, within the chunk-length floor of its kernel
@@ -344,8 +385,11 @@ int gemm_split(phx_kernel k, int64_t M, int64_t N, int64_t K) {
     const int64_t tiles = ((M + PHX_H_BM - 1) / PHX_H_BM) * ((N + PHX_H_BN - 1) / PHX_H_BN);
     const int64_t steps = (K + PHX_SPLIT_KSTEP - 1) / PHX_SPLIT_KSTEP;
     int64_t sp;
+    phx_plan pin;
     if (const char *env = getenv("PHX_GEMM_SPLIT")) {
         sp = atoi(env);
+    } else if (pinned_plan(gemm_key(k, M, N, K), &pin)) {
+        sp = pin.splits;
     } else {
         if (tiles >= PHX_SPLIT_MIN_TILES) return 1;
         const int64_t min_steps =
@@ -369,8 +413,12 @@ int gemm_split(phx_kernel k, int64_t M, int64_t N, int64_t K) {
 // measurement.
 static bool gemm_w8(phx_kernel k, int64_t M, int64_t N, int64_t K) {
     if (k != PHX_GEMM_FP16TC_FP32ACC) return false;
-    if (const char *env = getenv("PHX_GEMM_W8"))
+    phx_plan pin;
+    if (const char *env = getenv("PHX_GEMM_W8")) {
         if (atoi(env) == 0) return false;
+    } else if (pinned_plan(gemm_key(k, M, N, K), &pin) && pin.variant == 1) {
+        return false;
+    }
     return M % PHX_H_BM == 0 && N % PHX_H_BN == 0 && K % PHX_H_BK == 0;
 }
 
@@ -435,8 +483,11 @@ int flash_split(phx_kernel k, int64_t BH, int64_t Nq, int64_t Nk) {
     const int64_t items = ((Nq + qb - 1) / qb) * BH;
     const int64_t nkb = (Nk + PHX_FA_BC - 1) / PHX_FA_BC;
     int64_t sp;
+    phx_plan pin;
     if (const char *env = getenv("PHX_FLASH_SPLIT")) {
         sp = atoi(env);
+    } else if (pinned_plan(flash_key(k, BH, Nq, Nk), &pin)) {
+        sp = pin.splits;
     } else {
         if (2 * items >= PHX_FA_SLOTS) return 1;
         sp = PHX_FA_SLOTS / items;
@@ -952,6 +1003,55 @@ int phx_split_plan(phx_kernel k, const int64_t *dims, int ndims, int *splits,
     }
     if (splits) *splits = sp;
     if (workspace_bytes) *workspace_bytes = ws;
+    return PHX_OK;
+}
+
+int phx_plan_get(phx_kernel k, const int64_t *dims, int ndims, phx_plan *plan) {
+    if (!plan) return set_error(PHX_E_INVALID, "null plan");
+    if (int rc = check_shape(k, dims, ndims)) return rc;
+    plan->splits = 1;
+    plan->variant = 0;
+    if (is_gemm(k)) {
+        plan->splits = gemm_split(k, dims[0], dims[1], dims[2]);
+        if (k == PHX_GEMM_FP16TC_FP32ACC && plan->splits == 1 &&
+            !gemm_w8(k, dims[0], dims[1], dims[2]))
+            plan->variant = 1;
+    } else if (is_flash(k)) {
+        const bool bh = ndims == 4;
+        plan->splits = flash_split(k, bh ? dims[0] : 1, dims[bh], dims[bh + 1]);
+    }
+    return PHX_OK;
+}
+
+int phx_plan_pin(phx_kernel k, const int64_t *dims, int ndims, const phx_plan *plan) {
+    if (int rc = check_shape(k, dims, ndims)) return rc;
+    PlanKey key;
+    if (is_gemm(k)) {
+        key = gemm_key(k, dims[0], dims[1], dims[2]);
+    } else if (is_flash(k)) {
+        const bool bh = ndims == 4;
+        key = flash_key(k, bh ? dims[0] : 1, dims[bh], dims[bh + 1]);
+    } else {
+        return set_error(PHX_E_INVALID, "kernel %d has no launch plan choices", (int)k);
+    }
+    if (plan) {
+        if (plan->splits < 1 || plan->splits > PHX_SPLIT_MAX)
+            return set_error(PHX_E_INVALID, "splits %d outside 1..%d", plan->splits, PHX_SPLIT_MAX);
+        if (plan->variant != 0 && !(k == PHX_GEMM_FP16TC_FP32ACC && plan->variant == 1))
+            return set_error(PHX_E_INVALID, "variant %d: kernel %d has no such variant",
+                             plan->variant, (int)k);
+    }
+    std::lock_guard<std::mutex> lock(g_plan_mu);
+    if (plan)
+        g_plans[key] = *plan;
+    else
+        g_plans.erase(key);
+    return PHX_OK;
+}
+
+int phx_plan_unpin_all(void) {
+    std::lock_guard<std::mutex> lock(g_plan_mu);
+    g_plans.clear();
     return PHX_OK;
 }
 

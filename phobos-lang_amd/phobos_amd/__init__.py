@@ -134,6 +134,10 @@ def lib():
     L.phx_check_shape.argtypes = [ctypes.c_int, ctypes.POINTER(_i64), ctypes.c_int]
     L.phx_split_plan.argtypes = [ctypes.c_int, ctypes.POINTER(_i64), ctypes.c_int,
                                  ctypes.POINTER(ctypes.c_int), ctypes.POINTER(_sz)]
+    L.phx_plan_get.argtypes = [ctypes.c_int, ctypes.POINTER(_i64), ctypes.c_int,
+                               ctypes.POINTER(Plan)]
+    L.phx_plan_pin.argtypes = [ctypes.c_int, ctypes.POINTER(_i64), ctypes.c_int,
+                               ctypes.POINTER(Plan)]
     L.phx_compute.argtypes = [_vp, ctypes.c_int, ctypes.POINTER(TileArg), ctypes.c_uint32,
                               ctypes.POINTER(ScalarArg), ctypes.c_uint32, _u32a3, _u32a3, _vp]
     L.phx_saxpy.argtypes = [_vp, _u64, _u64, _u64, _i64, ctypes.c_float]
@@ -374,6 +378,30 @@ def split_plan(kernel, dims):
     sp, ws = ctypes.c_int(), _sz()
     check(lib().phx_split_plan(kernel, d, len(dims), ctypes.byref(sp), ctypes.byref(ws)))
     return sp.value, ws.value
+
+
+class Plan(ctypes.Structure):
+    """phx_plan: K or key chunks (1 = unsplit) and kernel variant."""
+    _fields_ = [("splits", ctypes.c_int32), ("variant", ctypes.c_int32)]
+
+
+def plan_get(kernel, dims):
+    """(splits, variant) a launch of kernel over dims uses now (phx_plan_get)."""
+    d = (_i64 * len(dims))(*dims)
+    p = Plan()
+    check(lib().phx_plan_get(kernel, d, len(dims), ctypes.byref(p)))
+    return p.splits, p.variant
+
+
+def plan_pin(kernel, dims, splits=None, variant=0):
+    """Pins (splits, variant) for kernel at dims; splits None removes the pin."""
+    d = (_i64 * len(dims))(*dims)
+    p = None if splits is None else ctypes.byref(Plan(splits, variant))
+    check(lib().phx_plan_pin(kernel, d, len(dims), p))
+
+
+def plan_unpin_all():
+    check(lib().phx_plan_unpin_all())
 
 
 def kernel_abi(kernel):

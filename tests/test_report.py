@@ -62,6 +62,10 @@ def test_bench_cli_mirrors_phobos_bench_flags():
     r = run("--bench", "gemm_fp8")
     assert r.returncode == 2 and "available: saxpy_fp32, gemm_fp32" in r.stderr
     r = run("--bench", "gemm_fp16", "--autotune", "TILE_M=256")
-    assert r.returncode == 2 and "no search to pin" in r.stderr
+    assert r.returncode == 2 and "'TILE_M' is not a search dim" in r.stderr
+    r = run("--autotune", "splits=2")
+    assert r.returncode == 2 and "pass --bench to pick one" in r.stderr
+    r = run("--bench", "gemm_fp16", "--autotune", "splits=two")
+    assert r.returncode == 2 and "non-integer value 'two'" in r.stderr
     r = run("--help")
     assert r.returncode == 0 and "--bench NAME" in r.stdout and "--csv" in r.stdout
