@@ -73,17 +73,22 @@ class Autotuner:
     """autotune.rs Autotuner: launch() runs the kernel once on stream under
     the pinned plan; verify() is called after a plan's first launch and
     raises AssertionError if that plan's output is wrong (it may launch again
-    from restored inputs, as the GEMM's C is read and written)."""
+    from restored inputs, as the GEMM's C is read and written); reset(), if
+    given, restores the inputs before each timed probe, outside the timing
+    (a GEMM with beta != 0 would otherwise grow C by beta every launch)."""
 
     def __init__(self, stream, kernel, dims, launch, verify, short_probes=3, long_probes=10,
-                 finalists=3):
+                 finalists=3, reset=None):
         self.stream, self.kernel, self.dims = stream, kernel, list(dims)
-        self.launch, self.verify = launch, verify
+        self.launch, self.verify, self.reset = launch, verify, reset
         self.short_probes, self.long_probes, self.finalists = short_probes, long_probes, finalists
         self.e0, self.e1 = Event(), Event()
 
     def _time(self, reps=1):
         """Average seconds per launch over reps back-to-back launches."""
+        if self.reset is not None:
+            self.stream.synchronize()  # nothing may still be writing what reset() restores
+            self.reset()
         self.e0.record(self.stream)
         for _ in range(reps):
             self.launch()
@@ -181,7 +186,8 @@ def tune_gemm(stream, kernel, M, N, K, alpha=1.0, beta=0.0, seed=1, **kw):
         stream.synchronize()
         _close(result(), want, tol)
 
-    tuner = Autotuner(stream, kernel, dims, run_once, verify, **kw)
+    reset = None if beta == 0.0 else (lambda: C.upload(c0))
+    tuner = Autotuner(stream, kernel, dims, run_once, verify, reset=reset, **kw)
     return tuner.run(gemm_space(kernel, M, N, K))
 
 
