@@ -137,3 +137,33 @@ def test_manifest_encoder_is_canonical_protobuf():
     for idx, h, name in kernels:
         ref.kernels.add(index=idx, hash=h, name=name)
     assert ours == ref.SerializeToString()
+
+
+def test_decoder_survives_corrupt_input():
+    # Mutated, truncated, extended and random encodings: the decoder returns
+    # a segment or an error for each, and never reads out of bounds (a crash
+    # would end the test run).  Seeded, so the cases are the same every run.
+    import random
+    ins = cluster.lower_matmul(1024, 2048, 1024, 512, 1024, 256, 0.125, 1.5)
+    base = segment_from_instrs(ins, 3).SerializeToString()
+    rng = random.Random(20261201)
+    decoded = refused = 0
+    for _ in range(3000):
+        d = bytearray(base)
+        kind = rng.randrange(4)
+        if kind == 0:
+            for _ in range(rng.randrange(1, 8)):
+                d[rng.randrange(len(d))] = rng.randrange(256)
+        elif kind == 1:
+            d = d[:rng.randrange(len(d))]
+        elif kind == 2:
+            d = bytearray(rng.randrange(256) for _ in range(rng.randrange(64)))
+        else:
+            at = rng.randrange(len(d))
+            d[at:at] = bytes(rng.randrange(256) for _ in range(rng.randrange(1, 16)))
+        try:
+            px.segment_pb_to_text(bytes(d))
+            decoded += 1
+        except px.PhxError:
+            refused += 1
+    assert decoded + refused == 3000 and refused > 0
