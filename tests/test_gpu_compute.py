@@ -193,3 +193,96 @@ def test_launch_by_reference_names_with_void_args(px_gpu, stream):
     # unknown names are refused before any launch
     assert px.lib().phx_launch_by_name(b"gemm_fp64", b"gemm", grid, None, stream.handle, args) \
         == px.PHX_E_INVALID
+
+
+_THREADS_SCRIPT = r'''
+import sys, threading
+import numpy as np
+sys.path[:0] = sys.argv[1:3]
+import oracle
+import phobos_amd as px
+px.init(0)
+errors = []
+start = threading.Barrier(6)
+
+def gemm(kern, f16):
+    M, N, K = 300, 200, 512
+    A = oracle.normal_f32(5, M * K, 1 / np.sqrt(K)).reshape(M, K)
+    B = oracle.normal_f32(6, K * N, 1 / np.sqrt(K)).reshape(K, N)
+    if kern != px.GEMM_FP32:
+        A, B = oracle.f16_round(A), oracle.f16_round(B)
+    conv = oracle.f16_bits if f16 else (lambda t: np.ascontiguousarray(t, np.float32))
+    da, db = px.DeviceBuffer.from_array(conv(A)), px.DeviceBuffer.from_array(conv(B))
+    dc = px.DeviceBuffer(M * N * (2 if f16 else 4))
+    want = oracle.gemm_full(A, B, None, 1.0, 0.0, round16=kern != px.GEMM_FP32)
+    def run(s):
+        px.launch_gemm(s, kern, da, db, dc, M, N, K, 1.0, 0.0)
+        s.synchronize()
+        r = dc.download(np.uint16 if f16 else np.float32, M * N)
+        return (oracle.f16_to_f32(r) if f16 else r).reshape(M, N)
+    tol = 2e-2 if kern != px.GEMM_FP32 else 1e-4
+    return run, lambda g: np.abs(g - want).max() / np.sqrt(np.mean(want ** 2)) < tol
+
+def flash(kern, f16):
+    Nq, Nk, D = 256, 1000, 64
+    q, k, v = (oracle.normal_f32(s, n * D).reshape(n, D) for s, n in ((7, Nq), (8, Nk), (9, Nk)))
+    if f16:
+        q, k, v = (oracle.f16_round(t) for t in (q, k, v))
+    conv = oracle.f16_bits if f16 else (lambda t: np.ascontiguousarray(t, np.float32))
+    dq, dk, dv = (px.DeviceBuffer.from_array(conv(t)) for t in (q, k, v))
+    do = px.DeviceBuffer(Nq * D * (2 if f16 else 4))
+    rows = np.arange(0, Nq, 17)
+    want = oracle.flash_rows(rows, q, k, v, 0.125)
+    def run(s):
+        px.launch_flash(s, kern, dq, dk, dv, do, Nq, Nk, D, 0.125)
+        s.synchronize()
+        r = do.download(np.uint16 if f16 else np.float32, Nq * D)
+        return (oracle.f16_to_f32(r) if f16 else r).reshape(Nq, D)
+    tol = 2e-2 if f16 else 1e-4
+    return run, lambda g: (np.abs(g[rows] - want) / np.maximum(np.abs(want), 0.1)).max() < tol
+
+def saxpy():
+    n = 100003
+    x, y = oracle.lcg_f32(1, n), oracle.lcg_f32(2, n)
+    dx, dy, do = px.DeviceBuffer.from_array(x), px.DeviceBuffer.from_array(y), px.DeviceBuffer(4 * n)
+    want = oracle.saxpy(2.5, x, y)
+    def run(s):
+        px.launch_saxpy(s, dx, dy, do, n, 2.5)
+        s.synchronize()
+        return do.download(np.float32, n)
+    return run, lambda g: np.array_equal(g.view(np.uint32), want.view(np.uint32))
+
+jobs = [saxpy(), gemm(px.GEMM_FP32, False), gemm(px.GEMM_FP16TC_FP32ACC, False),
+        gemm(px.GEMM_FP16, True), flash(px.FLASH_FP32, False), flash(px.FLASH_FP16, True)]
+
+def worker(i):
+    try:
+        s = px.Stream()
+        run, ok = jobs[i]
+        start.wait()  # every thread's first launch (and code-object load) at once
+        first = run(s)
+        assert ok(first), f"job {i}: wrong result"
+        for _ in range(10):
+            assert np.array_equal(run(s), first), f"job {i}: result changed"
+    except Exception as e:
+        errors.append(repr(e))
+
+ts = [threading.Thread(target=worker, args=(i,)) for i in range(6)]
+[t.start() for t in ts]
+[t.join() for t in ts]
+print("ERRORS" if errors else "OK", errors, flush=True)
+sys.exit(1 if errors else 0)
+'''
+
+
+def test_concurrent_first_launches_from_threads(px_gpu):
+    # Six host threads, each with its own stream, start at once in a fresh
+    # process, so six code objects load concurrently on first use; each
+    # result matches the oracle and stays the same over ten more launches.
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, "-c", _THREADS_SCRIPT, root,
+                        os.path.join(root, "phobos-lang_amd")],
+                       capture_output=True, text=True, timeout=180)
+    assert r.returncode == 0 and "OK" in r.stdout, (r.stdout, r.stderr[-2000:])
