@@ -300,10 +300,16 @@ def autotune_leg(px, stream, wanted, pins):
             out[name] = {"pinned": list(px.plan_get(kid, pdims))}
             continue
         t0 = time.perf_counter()
-        if kind == "gemm":
-            r = autotune.tune_gemm(stream, kid, *dims, **kw)
-        else:
-            r = autotune.tune_flash(stream, kid, *dims)
+        try:
+            if kind == "gemm":
+                r = autotune.tune_gemm(stream, kid, *dims, **kw)
+            else:
+                r = autotune.tune_flash(stream, kid, *dims)
+        except px.PhxError as e:  # keep the built-in plan; the timed steps still run
+            px.plan_pin(kid, pdims, None)
+            out[name] = {"error": str(e), "plan": list(px.plan_get(kid, pdims))}
+            log(f"autotune {name} failed ({e}); built-in plan {out[name]['plan']}")
+            continue
         out[name] = {"winner": list(r["winner"]), "us": round(r["us"], 2),
                      "finalists": [[list(f["plan"]), round(f["us"], 2)] for f in r["stage2"]],
                      "plans_tried": len(r["stage1"]), "s": round(time.perf_counter() - t0, 2)}
