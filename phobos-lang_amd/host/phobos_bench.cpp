@@ -279,11 +279,11 @@ struct Args {
         push(p);
         push(p);
         idx(bits, 0);
-        for (int64_t s : sizes) idx(bits, s);
-        int64_t stride = 1;
-        std::vector<int64_t> st;
-        for (auto it = sizes.end(); it != sizes.begin();) st.insert(st.begin(), stride), stride *= *--it;
-        for (int64_t s : st) idx(bits, s);
+        const std::vector<int64_t> sz(sizes);
+        for (int64_t s : sz) idx(bits, s);
+        std::vector<int64_t> stride(sz.size(), 1);  // row-major
+        for (size_t d = sz.size() - 1; d-- > 0;) stride[d] = stride[d + 1] * sz[d + 1];
+        for (int64_t s : stride) idx(bits, s);
     }
     void **list() {
         ptrs.clear();
