@@ -1,0 +1,105 @@
+"""The launch-plan rules and pins of the C ABI (phx_split_plan, phx_plan_get,
+phx_plan_pin) on the CPU: they are host logic, so no device is needed.  The
+split rule is restated here independently (phx_geometry.h's constants:
+256 x 256 output tiles, 32-deep K steps, at least 128 tiles or 256 of 512
+flash slots before anything splits, at most 16 chunks, at least 1 K step per
+chunk for gemm_fp32 and 32 for the f16 GEMMs, at least 8 key blocks per flash
+chunk, no empty chunk) and compared over a grid of shapes."""
+import itertools
+
+import pytest
+
+import phobos_amd as px
+
+
+@pytest.fixture(autouse=True)
+def _unpin():
+    px.plan_unpin_all()
+    yield
+    px.plan_unpin_all()
+
+
+def _rounded(units, sp):
+    sp = min(sp, units)
+    if sp < 2:
+        return 1
+    per = -(-units // sp)
+    return -(-units // per)
+
+
+def _gemm_rule(kern, M, N, K):
+    tiles = -(-M // 256) * -(-N // 256)
+    steps = -(-K // 32)
+    if tiles >= 128:
+        return 1
+    sp = min(256 // tiles, steps // (1 if kern == px.GEMM_FP32 else 32), 16)
+    return _rounded(steps, sp)
+
+
+def _flash_rule(f16, BH, Nq, Nk):
+    items = -(-Nq // (256 if f16 else 128)) * BH
+    nkb = -(-Nk // 64)
+    if 2 * items >= 512:
+        return 1
+    return _rounded(nkb, min(512 // items, nkb // 8, 16))
+
+
+GEMMS = ["GEMM_FP32", "GEMM_FP16TC_FP32ACC", "GEMM_FP16"]
+
+
+@pytest.mark.parametrize("name", GEMMS)
+def test_gemm_split_rule(name):
+    kern = getattr(px, name)
+    for M, N, K in itertools.product((64, 256, 300, 1024, 2048, 4096), (256, 512, 4096),
+                                     (64, 512, 1000, 4096, 16384)):
+        if kern != px.GEMM_FP32 and K % 8:
+            continue
+        want = _gemm_rule(kern, M, N, K)
+        sp, ws = px.split_plan(kern, [M, N, K])
+        assert sp == want, (M, N, K, sp, want)
+        assert ws == (sp * M * N * 4 if sp > 1 else 0)
+        assert px.plan_get(kern, [M, N, K])[0] == want
+
+
+@pytest.mark.parametrize("f16", [True, False])
+def test_flash_split_rule(f16):
+    one, bh = (px.FLASH_FP16, px.FLASH_FP16_BH) if f16 else (px.FLASH_FP32, px.FLASH_FP32_BH)
+    for BH, Nq, Nk in itertools.product((1, 2, 16, 64), (64, 300, 4096), (64, 700, 4096, 16384)):
+        want = _flash_rule(f16, BH, Nq, Nk)
+        sp, ws = px.split_plan(bh, [BH, Nq, Nk, 64])
+        assert sp == want, (BH, Nq, Nk, sp, want)
+        assert ws == (sp * BH * Nq * 66 * 4 if sp > 1 else 0)
+        if BH == 1:
+            assert px.split_plan(one, [Nq, Nk, 64])[0] == want
+
+
+def test_pins_override_the_rule_and_come_off():
+    dims = [512, 512, 4096]
+    rule = px.plan_get(px.GEMM_FP32, dims)
+    px.plan_pin(px.GEMM_FP32, dims, 3)
+    assert px.plan_get(px.GEMM_FP32, dims) == (3, 0)
+    assert px.split_plan(px.GEMM_FP32, dims) == (3, 3 * 512 * 512 * 4)
+    with pytest.raises(px.PhxError, match="outside 1..16"):
+        px.plan_pin(px.GEMM_FP32, dims, 500)
+    assert px.plan_get(px.GEMM_FP32, dims) == (3, 0)  # a refused pin leaves the old one
+    px.plan_pin(px.GEMM_FP32, dims, None)
+    assert px.plan_get(px.GEMM_FP32, dims) == rule
+
+
+def test_pin_validation():
+    dims = [512, 512, 4096]
+    for sp, var in ((0, 0), (17, 0), (1, 1), (1, -1)):
+        with pytest.raises(px.PhxError):
+            px.plan_pin(px.GEMM_FP32, dims, sp, var)
+    px.plan_pin(px.GEMM_FP16TC_FP32ACC, dims, 1, 1)
+    assert px.plan_get(px.GEMM_FP16TC_FP32ACC, dims) == (1, 1)
+    # a pinned count is rounded like a requested one (whole steps, no empty chunk)
+    px.plan_pin(px.GEMM_FP32, [512, 512, 96], 16)
+    assert px.plan_get(px.GEMM_FP32, [512, 512, 96])[0] == 3
+    # one-head and batched flash share a pin; other heads counts do not
+    px.plan_pin(px.FLASH_FP16, [4096, 4096, 64], 4)
+    assert px.plan_get(px.FLASH_FP16_BH, [1, 4096, 4096, 64]) == (4, 0)
+    assert px.plan_get(px.FLASH_FP16_BH, [2, 4096, 4096, 64])[0] == _flash_rule(True, 2, 4096, 4096)
+    assert px.plan_get(px.FLASH_FP32, [4096, 4096, 64])[0] == _flash_rule(False, 1, 4096, 4096)
+    px.plan_pin(px.FLASH_FP16, [4096, 4096, 64], None)
+    assert px.plan_get(px.FLASH_FP16, [4096, 4096, 64])[0] == _flash_rule(True, 1, 4096, 4096)
