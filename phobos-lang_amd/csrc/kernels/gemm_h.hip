@@ -747,11 +747,17 @@ extern "C" __global__ __launch_bounds__(256) void gemm_splitk_reduce(const float
 // (same box, alternating), bit-identical output.  Probe builds put the rest
 // on the load path: without the MFMAs 105 us, without the loads 90 us.
 #define W8_NT 512
-// MFMA positions (of 8 per half step) of the A and B chunks
+// MFMA positions (of 8 per half step) of the A and B chunks, and of the
+// first of the six operand reads for the other slice
+#ifndef W8_A0
 #define W8_A0 0
 #define W8_A1 4
 #define W8_B0 0
 #define W8_B1 4
+#endif
+#ifndef W8_RD
+#define W8_RD 1
+#endif
 #define W8_WM 128
 #define W8_WN 64
 
@@ -871,7 +877,7 @@ __device__ __forceinline__ void w8_step(phx_f16v (&acc)[4][2], Frags8 &F0, Frags
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
         w8_mfma(acc, F0, m);
-        if (m < 6) w8_read(F1, cur, 1, wm, wn, lane, m);
+        if (m >= W8_RD && m < W8_RD + 6) w8_read(F1, cur, 1, wm, wn, lane, m - W8_RD);
         if (m == W8_A0 || m == W8_A1) w8_chunk(R, fill, ra, rb, voa, vob, lda, ldb, tid, m == W8_A0 ? 0 : 1);
         __builtin_amdgcn_sched_barrier(0);
     }
@@ -881,7 +887,7 @@ __device__ __forceinline__ void w8_step(phx_f16v (&acc)[4][2], Frags8 &F0, Frags
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
         w8_mfma(acc, F1, m);
-        if (m < 6) w8_read(F0, nxt, 0, wm, wn, lane, m);
+        if (m >= W8_RD && m < W8_RD + 6) w8_read(F0, nxt, 0, wm, wn, lane, m - W8_RD);
         if (m == W8_B0 || m == W8_B1) w8_chunk(R, fill, ra, rb, voa, vob, lda, ldb, tid, m == W8_B0 ? 2 : 3);
         __builtin_amdgcn_sched_barrier(0);
     }
