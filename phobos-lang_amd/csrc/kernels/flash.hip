@@ -178,8 +178,8 @@ __device__ __forceinline__ float softmax_c2(float scale) {
 //
 // K and V blocks are copied global -> LDS directly (buffer_load ... lds, 16
 // bytes per lane; each wave copies 8 rows of K and 8 of V) into a ring of 4
-// stages (K 8 KiB + V 8 KiB each): block i+3 is issued when block i starts,
-// and one barrier per block publishes it.
+// stages (K 8 KiB + V 8 KiB each): block i+3 is issued during block i (after
+// its softmax), and one barrier per block publishes it.
 #define WQ 32                  // queries per wave
 #define NWAVE 8
 #define QB (NWAVE * WQ)        // queries per workgroup
@@ -369,11 +369,14 @@ __device__ __forceinline__ void flash16_step(Flash16 &fs, const char *cur, char 
     PHX_WAIT_VM_LGKM0((NSTAGE - 2) * DMA_PER_BLK);  // own copies of block i landed
     __builtin_amdgcn_s_barrier();                     // everyone's block i landed, i-1 done
     __builtin_amdgcn_sched_barrier(0);
-    dma_block(fill, Kp, Vp, ldk, ldv, Nk, i + NSTAGE - 1, vk, vv, wave);
     phx_f16v sc[2];
     scores(sc, cur, fs, lq, g);
     phx_h8 pf[4];
     float ps = softmax_p(pf, sc, c2, fs.m2);
+    // block i+3's copies go out between the softmax and P.V, not at the top
+    // of the step next to the score MFMAs' K reads: 298.6 against 306.1 us
+    // on average over five alternations on one box, bit-identical
+    dma_block(fill, Kp, Vp, ldk, ldv, Nk, i + NSTAGE - 1, vk, vv, wave);
     const bool slow = FIRST || __ballot(!(ps <= FAST_SUM_LIMIT));  // wave-uniform; NaN too
     if (slow) {
 #pragma unroll
