@@ -370,14 +370,25 @@ __device__ __forceinline__ void flash16_step(Flash16 &fs, const char *cur, char 
     __builtin_amdgcn_s_barrier();                     // everyone's block i landed, i-1 done
     __builtin_amdgcn_sched_barrier(0);
     phx_f16v sc[2];
-    scores(sc, cur, fs, lq, g);
     phx_h8 pf[4];
+    if constexpr (FIRST) {  // m2 starts at block 0's row max: no fast path to try
+        key_bias(sc, Nk < BC ? Nk : BC, g);  // block 0 may be partial: keys past Nk are -inf
+        scores<true>(sc, cur, fs, lq, g);
+        const float mx = row_max(sc) * c2;  // log2 units
+        const float ps = softmax_p(pf, sc, c2, mx);
+        dma_block(fill, Kp, Vp, ldk, ldv, Nk, i + NSTAGE - 1, vk, vv, wave);
+        fs.m2 = mx;
+        fs.l += ps;
+        pv(fs.acc, cur + KV_TILE, pf, lane);
+        return;
+    }
+    scores(sc, cur, fs, lq, g);
     float ps = softmax_p(pf, sc, c2, fs.m2);
     // block i+3's copies go out between the softmax and P.V, not at the top
     // of the step next to the score MFMAs' K reads: 298.6 against 306.1 us
     // on average over five alternations on one box, bit-identical
     dma_block(fill, Kp, Vp, ldk, ldv, Nk, i + NSTAGE - 1, vk, vv, wave);
-    const bool slow = FIRST || __ballot(!(ps <= FAST_SUM_LIMIT));  // wave-uniform; NaN too
+    const bool slow = __ballot(!(ps <= FAST_SUM_LIMIT));  // wave-uniform; NaN too
     if (slow) {
 #pragma unroll
         for (int c = 0; c < 4; ++c) pf[c] = (phx_h8){0, 0, 0, 0, 0, 0, 0, 0};
@@ -386,21 +397,14 @@ __device__ __forceinline__ void flash16_step(Flash16 &fs, const char *cur, char 
     }
     pv(fs.acc, cur + KV_TILE, pf, lane);
     if (slow) {
-        if (FIRST) {  // block 0 may be partial (Nk < 64): keys past Nk start from -inf
-            key_bias(sc, Nk < BC ? Nk : BC, g);
-            scores<true>(sc, cur, fs, lq, g);
-        } else {
-            scores(sc, cur, fs, lq, g);
-        }
+        scores(sc, cur, fs, lq, g);
         const float mx = row_max(sc) * c2;  // block row max, log2 units
-        const float m2n = (FIRST || mx > fs.m2 + RESCALE_SLACK) ? mx : fs.m2;
+        const float m2n = mx > fs.m2 + RESCALE_SLACK ? mx : fs.m2;
         ps = softmax_p(pf, sc, c2, m2n);
-        if (!FIRST) {
-            const float corr = __builtin_amdgcn_exp2f(fs.m2 - m2n);  // 1 where not raised
-            fs.l = fs.l * corr;
-            fs.acc[0] = fs.acc[0] * corr;
-            fs.acc[1] = fs.acc[1] * corr;
-        }
+        const float corr = __builtin_amdgcn_exp2f(fs.m2 - m2n);  // 1 where not raised
+        fs.l = fs.l * corr;
+        fs.acc[0] = fs.acc[0] * corr;
+        fs.acc[1] = fs.acc[1] * corr;
         fs.m2 = m2n;
         fs.l += ps;
         pv(fs.acc, cur + KV_TILE, pf, lane);
