@@ -213,6 +213,13 @@ def setup(px, stream, wanted):
     return ks
 
 
+# Split launches keep their partial results in the workspace bound to their
+# stream (the launches never allocate): a buffer this host allocates once,
+# enough for 16 chunks of a 4096 x 4096 f32 output or of the 64-head flash
+# state.  The autotuner binds a larger one if its search needs it.
+WORKSPACE_BYTES = 2 << 30
+
+
 def shapes_leg(px, stream, reps=20, tune=True):
     """Time the shapes that run split (phx_split_plan): each GEMM at 512^3 and
     1024^3, and the one-head flash .ph entry (main.rs:334-371) at 4096 x 4096.
@@ -526,7 +533,9 @@ def main():
     info = px.device_info()
     log(f"device: {info}")
     if args.shapes:
-        res = shapes_leg(px, px.Stream(), tune=not args.no_autotune)
+        sstream = px.Stream()
+        px.bind_workspace(sstream, WORKSPACE_BYTES)
+        res = shapes_leg(px, sstream, tune=not args.no_autotune)
         for r in res:
             log(f"{r['kernel']:28s} {str(r['shape']):18s} splits {r['splits']:2d}  "
                 f"{r['us']:8.2f} us  {r['tflops']:8.2f} TFLOP/s  autotuned {r['autotuned']}")
@@ -536,6 +545,7 @@ def main():
                  "flash_fp16"]
     wanted = all_names if args.kernels == "all" else args.kernels.split(",")
     stream = px.Stream()
+    px.bind_workspace(stream, WORKSPACE_BYTES)
     tuned = None
     if not args.no_autotune and not args.hold:
         tuned = autotune_leg(px, stream, wanted, args.pins)

@@ -6,7 +6,11 @@
  * Every function returns 0 on success or a nonzero status (a HIP error code
  * where one exists, else PHX_E_*); phx_last_error() returns the message for
  * the calling thread.  No function here allocates device memory except the
- * ones named *_malloc / *_create.
+ * ones named *_malloc / *_create, phx_init and the lazy load of a code object
+ * on a kernel's first use (phx_module_load_*, phx_builtin_function, a
+ * built-in's first launch).  Launches never allocate: a split launch's
+ * partial results go to the caller-owned workspace bound to its stream
+ * (phx_stream_set_workspace).
  *
  * The entry points replace, one for one, what the reference's host code does
  * through the cust CUDA driver API:
@@ -91,6 +95,20 @@ int phx_memset_async(uint64_t dst, int value, size_t bytes, phx_stream s);
 int phx_stream_create(phx_stream *s); /* non-blocking, default priority */
 int phx_stream_destroy(phx_stream s);
 int phx_stream_synchronize(phx_stream s);
+/* Binds a caller-owned device buffer (256-byte aligned) as the workspace of
+ * split launches on stream s (NULL: the legacy default stream); dptr 0 or
+ * bytes 0 unbinds.  No counterpart in the reference, whose kernels never
+ * split: it keeps the reference's ownership rule (the caller owns every
+ * device buffer, tile_store.rs:14-83; a COMPUTE touches only arena tiles,
+ * engine.rs:582-647) for the split launches of this backend.  A built-in
+ * GEMM or flash launch that phx_split_plan would split runs with the largest
+ * split whose workspace fits in the bound bytes, and unsplit when none fits
+ * or nothing is bound; it never allocates.  The buffer must stay valid until
+ * every launch on s that may use it has completed; launches on one stream
+ * run in order, so they can share it.  Unbinding (or phx_stream_destroy)
+ * forgets it; the caller frees it. */
+int phx_stream_set_workspace(phx_stream s, uint64_t dptr, size_t bytes);
+int phx_stream_get_workspace(phx_stream s, uint64_t *dptr, size_t *bytes);
 int phx_event_create(phx_event *e);
 int phx_event_destroy(phx_event e);
 int phx_event_record(phx_event e, phx_stream s);
@@ -119,8 +137,9 @@ int phx_kernel_abi(phx_kernel k, int *index_bits, uint32_t block[3]);
  * replaces grid, block and shared_bytes with its own (the reference caller's
  * saxpy 1024-thread blocks and flash @launch(128) are accepted).  A built-in
  * GEMM or flash launch whose problem cannot fill the GPU runs split over K
- * or over the keys (phx_split_plan), with a workspace taken from HIP's
- * stream-ordered memory pool and released on s. */
+ * or over the keys (phx_split_plan) when s has a workspace bound
+ * (phx_stream_set_workspace) that holds the split's partial results, else
+ * unsplit. */
 int phx_launch(phx_function f, const uint32_t grid[3], const uint32_t block[3],
                uint32_t shared_bytes, phx_stream s, void **args);
 
@@ -146,9 +165,11 @@ int phx_launch_by_name(const char *ph_file, const char *entry, const uint32_t gr
                        const uint32_t block[3], phx_stream s, void **args);
 /* Validates that a built-in kernel accepts these dims (divisibility etc). */
 int phx_check_shape(phx_kernel k, const int64_t *dims, int ndims);
-/* The split a launch of k over dims (as phx_grid_for) runs with: *splits K
+/* The split a launch of k over dims (as phx_grid_for) runs with on a stream
+ * whose bound workspace holds at least *workspace_bytes: *splits K
  * chunks (gemm_fp32, gemm_fp16tc_fp32acc, gemm_fp16) or key chunks (flash),
- * 1 for none, and the workspace bytes that needs (0 for none).  Other
+ * 1 for none, and the workspace bytes that needs (0 for none).  With a
+ * smaller workspace a launch takes fewer chunks, down to none.  Other
  * kernels never split.  No counterpart in the reference, whose autotuner
  * picks tile sizes instead (phobos-bench/src/autotune.rs:98-192). */
 int phx_split_plan(phx_kernel k, const int64_t *dims, int ndims, int *splits,
@@ -282,6 +303,10 @@ int phx_f16_to_f32(size_t n, const uint16_t *in, float *out);
 typedef struct phx_pod_s *phx_pod;
 int phx_pod_create(phx_pod *p, size_t arena_bytes, int nstreams);
 int phx_pod_destroy(phx_pod p);
+/* The pod's device arena (for phx_arena_stats); owned by the pod.  Besides
+ * the segment's tiles it holds the workspace of a split built-in COMPUTE
+ * while that leaf runs. */
+int phx_pod_get_arena(phx_pod p, phx_arena *a);
 /* Registers a tensor id -> (uri, shape) for LOAD/STORE (JobManifest). */
 int phx_pod_set_tensor(phx_pod p, uint32_t tensor, const char *uri, const uint64_t *shape,
                        uint32_t rank);

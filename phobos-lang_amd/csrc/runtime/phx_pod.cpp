@@ -206,6 +206,10 @@ struct Inflight {
     size_t chunk = 0;   // H2D / D2H: chunk of the tile
     hipEvent_t start = nullptr, done = nullptr;
     void *staging = nullptr;
+    // Kernel: the arena slab a split launch keeps its partial results in
+    // (0: none), released when the launch completes
+    uint64_t ws_addr = 0;
+    size_t ws_cls = 0;
 };
 
 // A file read (LOAD) or write (STORE) of one chunk that a worker finished.
@@ -849,6 +853,12 @@ int phx_pod_create(phx_pod *out, size_t arena_bytes, int nstreams) {
     return PHX_OK;
 }
 
+int phx_pod_get_arena(phx_pod p, phx_arena *a) {
+    if (!p || !a) return set_error(PHX_E_INVALID, "null pod or arena");
+    *a = p->arena;
+    return PHX_OK;
+}
+
 int phx_pod_destroy(phx_pod p) {
     if (!p) return PHX_OK;
     delete p->io;
@@ -1247,25 +1257,84 @@ static int run_instrs(phx_pod p, std::vector<Instr> &ins, uint64_t stats[8]) {
             hipStream_t s = p->streams[p->next_stream];
             p->next_stream = (p->next_stream + 1) % p->streams.size();
             Inflight fl{Inflight::Kernel, i};
+            // A built-in GEMM or flash leaf too small to fill the GPU runs
+            // split; its partial results take an arena slab, as any tile
+            // does (tile_store.rs:14-83), bound to the launch stream for this
+            // one launch.  When the arena cannot hold it the leaf runs unsplit.
+            size_t ws_bytes = 0;
+            if (kit != p->kernels.end()) {
+                const phx_kernel k = kit->second;
+                int64_t dims[4];
+                int nd = 0;
+                const bool gemm = k == PHX_GEMM_FP32 || k == PHX_GEMM_FP16TC_FP32ACC ||
+                                  k == PHX_GEMM_FP16;
+                const bool flash = k == PHX_FLASH_FP32 || k == PHX_FLASH_FP16 ||
+                                   k == PHX_FLASH_FP32_BH || k == PHX_FLASH_FP16_BH;
+                if (gemm && targs.size() == 3 && targs[0].rank == 2 && targs[1].rank == 2) {
+                    dims[0] = (int64_t)targs[0].shape[0];
+                    dims[1] = (int64_t)targs[1].shape[1];
+                    dims[2] = (int64_t)targs[0].shape[1];
+                    nd = 3;
+                } else if (flash && targs.size() == 4 && targs[0].rank == targs[1].rank &&
+                           (targs[0].rank == 2 || targs[0].rank == 3)) {
+                    const uint32_t r = targs[0].rank;
+                    if (r == 3) dims[nd++] = (int64_t)targs[0].shape[0];
+                    dims[nd++] = (int64_t)targs[0].shape[r - 2];
+                    dims[nd++] = (int64_t)targs[1].shape[r - 2];
+                    dims[nd++] = (int64_t)targs[0].shape[r - 1];
+                }
+                int sp = 1;
+                // a shape the kernel does not take leaves ws_bytes 0, and the
+                // launch below reports it
+                if (nd && phx_split_plan(k, dims, nd, &sp, &ws_bytes) != PHX_OK) ws_bytes = 0;
+                if (ws_bytes && phx_arena_can_alloc(p->arena, ws_bytes)) {
+                    if (int rc = phx_arena_alloc(p->arena, ws_bytes, &fl.ws_addr, &fl.ws_cls))
+                        return rc;
+                    if (int rc = phx_stream_set_workspace((phx_stream)s, fl.ws_addr, ws_bytes)) {
+                        phx_arena_free(p->arena, fl.ws_addr, fl.ws_cls);
+                        return rc;
+                    }
+                }
+            }
+            // the slab goes back to the arena on any failure before the
+            // launch is in flight
+            auto drop_ws = [&]() {
+                if (!fl.ws_addr) return;
+                (void)phx_stream_set_workspace((phx_stream)s, 0, 0);
+                phx_arena_free(p->arena, fl.ws_addr, fl.ws_cls);
+                fl.ws_addr = 0;
+            };
             hipError_t e;
-            if ((e = hipEventCreate(&fl.start)) != hipSuccess) return hip_error(e, "hipEventCreate");
+            if ((e = hipEventCreate(&fl.start)) != hipSuccess) {
+                drop_ws();
+                return hip_error(e, "hipEventCreate");
+            }
             if ((e = hipEventCreate(&fl.done)) != hipSuccess) {
                 (void)hipEventDestroy(fl.start);
+                drop_ws();
                 return hip_error(e, "hipEventCreate");
             }
             if ((e = hipEventRecord(fl.start, s)) != hipSuccess) {
                 (void)hipEventDestroy(fl.start);
                 (void)hipEventDestroy(fl.done);
+                drop_ws();
                 return hip_error(e, "hipEventRecord");
             }
-            if (int rc = phx_compute((phx_function)f, bits, targs.data(), (uint32_t)targs.size(),
-                                     I.scalars.data(), (uint32_t)I.scalars.size(), grid, block,
-                                     (phx_stream)s)) {
+            const int crc = phx_compute((phx_function)f, bits, targs.data(),
+                                        (uint32_t)targs.size(), I.scalars.data(),
+                                        (uint32_t)I.scalars.size(), grid, block, (phx_stream)s);
+            if (fl.ws_addr) (void)phx_stream_set_workspace((phx_stream)s, 0, 0);
+            if (crc) {
+                // a launch that failed to enqueue may still have enqueued its
+                // first kernel (split launches are two), so the slab is only
+                // released once the stream has drained
+                (void)hipStreamSynchronize(s);
                 (void)hipEventDestroy(fl.start);
                 (void)hipEventDestroy(fl.done);
-                return rc;
+                if (fl.ws_addr) phx_arena_free(p->arena, fl.ws_addr, fl.ws_cls);
+                return crc;
             }
-            inflight.push_back(fl);  // the error drain destroys its events from here on
+            inflight.push_back(fl);  // the error drain destroys its events and slab from here on
             if ((e = hipEventRecord(fl.done, s)) != hipSuccess) return hip_error(e, "hipEventRecord");
             return PHX_OK;
         }
@@ -1346,6 +1415,11 @@ static int run_instrs(phx_pod p, std::vector<Instr> &ins, uint64_t stats[8]) {
                 else if (hipEventElapsedTime(&b, f.start, f.done) == hipSuccess)
                     st[5] += (uint64_t)(b * 1e6);  // no origin: the plain duration
                 (void)hipEventDestroy(f.start);
+                if (f.ws_addr) {  // the split's slab; a release may unpark allocations
+                    phx_arena_free(p->arena, f.ws_addr, f.ws_cls);
+                    for (size_t a : parked_alloc) ready.insert(a);
+                    parked_alloc.clear();
+                }
                 st[2]++;
                 complete(f.idx);
             } else if (f.stage == Inflight::H2D) {
@@ -1402,6 +1476,7 @@ static int run_instrs(phx_pod p, std::vector<Instr> &ins, uint64_t stats[8]) {
         for (auto &f : inflight) {
             if (f.start) (void)hipEventDestroy(f.start);
             if (f.done) (void)hipEventDestroy(f.done);
+            if (f.ws_addr) phx_arena_free(p->arena, f.ws_addr, f.ws_cls);
         }
         p->stage_free = p->stage_all;  // nothing is in flight any more
         for (uint64_t id : allocated_here) {

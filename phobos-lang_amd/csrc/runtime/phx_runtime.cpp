@@ -376,6 +376,46 @@ PlanKey flash_key(phx_kernel k, int64_t BH, int64_t Nq, int64_t Nk) {
 }
 }  // namespace
 
+// Workspaces bound to streams by phx_stream_set_workspace: device memory
+// the caller owns (a pod's arena slab, a bench's buffer).  A split launch on
+// a stream takes its partial results from the stream's workspace and never
+// allocates; a stream without one, or with one too small for any split, runs
+// the unsplit kernel.
+namespace {
+struct Workspace {
+    uint64_t ptr = 0;
+    size_t bytes = 0;
+};
+std::mutex g_ws_mu;
+std::unordered_map<hipStream_t, Workspace> g_ws;
+
+Workspace stream_workspace(hipStream_t s) {
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    auto it = g_ws.find(s);
+    return it == g_ws.end() ? Workspace{} : it->second;
+}
+
+// Chunks a split of `units` (K steps or key blocks) into at most sp chunks of
+// whole units really makes: ceil(units / ceil(units / sp)), so no chunk is
+// empty.
+int round_split(int64_t units, int64_t sp) {
+    if (sp > units) sp = units;
+    if (sp < 2) return 1;
+    const int64_t per = (units + sp - 1) / sp;
+    return (int)((units + per - 1) / per);
+}
+
+// The largest split of at most sp chunks of `units` whose workspace,
+// bytes_per_chunk per chunk, fits in cap bytes; 1 when none does.
+int fit_split(int64_t units, int sp, size_t bytes_per_chunk, size_t cap) {
+    for (int64_t want = sp; want >= 2; --want) {
+        const int r = round_split(units, want);
+        if (r >= 2 && (size_t)r * bytes_per_chunk <= cap) return r;
+    }
+    return 1;
+}
+}  // namespace
+
 // How many K chunks a GEMM is split into (1: no split).  A GEMM whose
 // 256 x 256 output tiles cannot fill half of the 256 CUs gets enough chunks
 // to give every CU a workgroup, within the chunk-length floor of its kernel
@@ -398,11 +438,8 @@ int gemm_split(phx_kernel k, int64_t M, int64_t N, int64_t K) {
         if (sp > steps / min_steps) sp = steps / min_steps;
         if (sp > PHX_SPLIT_MAX) sp = PHX_SPLIT_MAX;
     }
-    if (sp > steps) sp = steps;
-    if (sp < 2) return 1;
     // chunks of whole steps; drop chunks the rounding left empty
-    const int64_t per = (steps + sp - 1) / sp;
-    return (int)((steps + per - 1) / per);
+    return round_split(steps, sp);
 }
 
 // Whether a gemm_fp16tc_fp32acc launch runs the eight-wave kernel gemm_w8
@@ -460,19 +497,13 @@ int launch_gemm_split_ws(phx_kernel k, const Desc *t, int64_t M, int64_t N, int6
     return PHX_OK;
 }
 
-// The same with a stream-ordered workspace taken from HIP's memory pool and
-// returned on the stream after the reduce, so concurrent launches on other
-// streams never share it.
-int launch_gemm_split(phx_kernel k, const Desc *t, int64_t M, int64_t N, int64_t K, float alpha,
-                      float beta, int sp, hipStream_t s) {
-    void *ws = nullptr;
-    hipError_t e = hipMallocAsync(&ws, gemm_split_bytes(M, N, sp), s);
-    if (e != hipSuccess) return hip_error(e, "hipMallocAsync(split-K workspace)");
-    int rc = launch_gemm_split_ws(k, t, M, N, K, alpha, beta, sp, s, (uint64_t)(uintptr_t)ws);
-    e = hipFreeAsync(ws, s);
-    if (rc) return rc;
-    if (e != hipSuccess) return hip_error(e, "hipFreeAsync(split-K workspace)");
-    return PHX_OK;
+// The split count a GEMM launch on a stream whose workspace holds cap bytes
+// runs with: gemm_split's plan, cut to what fits.
+static int gemm_split_fit(phx_kernel k, int64_t M, int64_t N, int64_t K, size_t cap) {
+    const int sp = gemm_split(k, M, N, K);
+    if (sp < 2) return 1;
+    const int64_t steps = (K + PHX_SPLIT_KSTEP - 1) / PHX_SPLIT_KSTEP;
+    return fit_split(steps, sp, gemm_split_bytes(M, N, 1), cap);
 }
 
 // How many key chunks a flash launch is split into (1: no split).
@@ -494,10 +525,7 @@ int flash_split(phx_kernel k, int64_t BH, int64_t Nq, int64_t Nk) {
         if (sp > nkb / PHX_FLASH_SPLIT_MIN_BLOCKS) sp = nkb / PHX_FLASH_SPLIT_MIN_BLOCKS;
         if (sp > PHX_SPLIT_MAX) sp = PHX_SPLIT_MAX;
     }
-    if (sp > nkb) sp = nkb;
-    if (sp < 2) return 1;
-    const int64_t per = (nkb + sp - 1) / sp;  // blocks per chunk; no empty chunk
-    return (int)((nkb + per - 1) / per);
+    return round_split(nkb, sp);  // whole blocks per chunk; no empty chunk
 }
 
 // Bytes of partial results a split flash launch needs: per chunk and query,
@@ -542,20 +570,11 @@ int launch_flash_split_ws(phx_kernel k, const Desc *t, int rank, int64_t BH, int
     return PHX_OK;
 }
 
-int launch_flash_split(phx_kernel k, const Desc *t, int rank, int64_t BH, int64_t Nq, int64_t Nk,
-                       float scale, int sp, hipStream_t s) {
-    void *ws = nullptr;
-    hipError_t e = hipMallocAsync(&ws, flash_split_bytes(BH, Nq, sp), s);
-    if (e != hipSuccess) return hip_error(e, "hipMallocAsync(split-key workspace)");
-    hipFunction_t fs, fc;
-    int rc = flash_split_functions(k, &fs, &fc);
-    if (!rc)
-        rc = launch_flash_split_ws(k, t, rank, BH, Nq, Nk, scale, sp, s, (uint64_t)(uintptr_t)ws,
-                                   fs, fc);
-    e = hipFreeAsync(ws, s);
-    if (rc) return rc;
-    if (e != hipSuccess) return hip_error(e, "hipFreeAsync(split-key workspace)");
-    return PHX_OK;
+static int flash_split_fit(phx_kernel k, int64_t BH, int64_t Nq, int64_t Nk, size_t cap) {
+    const int sp = flash_split(k, BH, Nq, Nk);
+    if (sp < 2) return 1;
+    const int64_t nkb = (Nk + PHX_FA_BC - 1) / PHX_FA_BC;
+    return fit_split(nkb, sp, flash_split_bytes(BH, Nq, 1), cap);
 }
 
 int launch_raw(hipFunction_t f, const uint32_t grid[3], const uint32_t block[3], uint32_t shmem,
@@ -572,12 +591,14 @@ int launch_raw(hipFunction_t f, const uint32_t grid[3], const uint32_t block[3],
         if (int rc = builtin_dims((phx_kernel)k, args, d, &nd, t)) return rc;
         if (k == PHX_GEMM_FP32 || k == PHX_GEMM_FP16TC_FP32ACC || k == PHX_GEMM_FP16) {
             if (int rc = check_shape((phx_kernel)k, d, nd)) return rc;
-            const int sp = gemm_split((phx_kernel)k, d[0], d[1], d[2]);
+            const Workspace w = stream_workspace(s);
+            const int sp = gemm_split_fit((phx_kernel)k, d[0], d[1], d[2], w.bytes);
             if (sp > 1) {
                 float alpha, beta;  // the two f32 scalars after the three memrefs
                 memcpy(&alpha, args[21], 4);
                 memcpy(&beta, args[22], 4);
-                return launch_gemm_split((phx_kernel)k, t, d[0], d[1], d[2], alpha, beta, sp, s);
+                return launch_gemm_split_ws((phx_kernel)k, t, d[0], d[1], d[2], alpha, beta, sp,
+                                            s, w.ptr);
             }
             if (gemm_w8((phx_kernel)k, d[0], d[1], d[2])) {
                 hipFunction_t fw;
@@ -594,11 +615,15 @@ int launch_raw(hipFunction_t f, const uint32_t grid[3], const uint32_t block[3],
             if (int rc = check_shape((phx_kernel)k, d, nd)) return rc;
             const bool bh = nd == 4;
             const int64_t BH = bh ? d[0] : 1, Nq = d[bh], Nk = d[bh + 1];
-            const int sp = flash_split((phx_kernel)k, BH, Nq, Nk);
+            const Workspace w = stream_workspace(s);
+            const int sp = flash_split_fit((phx_kernel)k, BH, Nq, Nk, w.bytes);
             if (sp > 1) {
                 float scale;  // the f32 scalar after the four memrefs
                 memcpy(&scale, args[bh ? 36 : 28], 4);
-                return launch_flash_split((phx_kernel)k, t, bh ? 3 : 2, BH, Nq, Nk, scale, sp, s);
+                hipFunction_t fs, fc;
+                if (int rc = flash_split_functions((phx_kernel)k, &fs, &fc)) return rc;
+                return launch_flash_split_ws((phx_kernel)k, t, bh ? 3 : 2, BH, Nq, Nk, scale, sp,
+                                             s, w.ptr, fs, fc);
             }
         }
         uint32_t g2[3], b2[3];
@@ -770,6 +795,10 @@ int phx_init(int device, const char *dir) {
 
 int phx_shutdown(void) {
     scratch_reset();
+    {
+        std::lock_guard<std::mutex> lock(g_ws_mu);
+        g_ws.clear();
+    }
     std::lock_guard<std::mutex> lock(g.mu);
     for (auto &kv : g.modules) (void)hipModuleUnload(kv.second);
     g.modules.clear();
@@ -857,8 +886,27 @@ int phx_stream_create(phx_stream *s) {
     return PHX_OK;
 }
 int phx_stream_destroy(phx_stream s) {
+    {
+        std::lock_guard<std::mutex> lock(g_ws_mu);
+        g_ws.erase((hipStream_t)s);
+    }
     hipError_t e = hipStreamDestroy((hipStream_t)s);
     return e == hipSuccess ? PHX_OK : hip_error(e, "hipStreamDestroy");
+}
+int phx_stream_set_workspace(phx_stream s, uint64_t dptr, size_t bytes) {
+    if (dptr & 255) return set_error(PHX_E_INVALID, "workspace must be 256-byte aligned");
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    if (!dptr || !bytes)
+        g_ws.erase((hipStream_t)s);
+    else
+        g_ws[(hipStream_t)s] = Workspace{dptr, bytes};
+    return PHX_OK;
+}
+int phx_stream_get_workspace(phx_stream s, uint64_t *dptr, size_t *bytes) {
+    const Workspace w = stream_workspace((hipStream_t)s);
+    if (dptr) *dptr = w.ptr;
+    if (bytes) *bytes = w.bytes;
+    return PHX_OK;
 }
 int phx_stream_synchronize(phx_stream s) {
     hipError_t e = hipStreamSynchronize((hipStream_t)s);

@@ -520,6 +520,18 @@ void verify_flash(const std::vector<float> &o, const std::vector<float> &q,
 }
 
 // ------------------------------------------------------------------ benches
+constexpr int PHX_SPLIT_CHUNKS_MAX = 16;  // the most chunks phx_plan_pin takes
+
+// A device buffer bound as the split workspace of a stream while it lives.
+struct Workspace {
+    Buf buf;
+    phx_stream s;
+    Workspace(phx_stream st, size_t bytes) : buf(bytes), s(st) {
+        check(phx_stream_set_workspace(s, buf.ptr, bytes), "phx_stream_set_workspace");
+    }
+    ~Workspace() { phx_stream_set_workspace(s, 0, 0); }
+};
+
 struct Ctx {
     const Options &opt;
     phx_stream stream;
@@ -590,6 +602,9 @@ void bench_gemm(Ctx &cx, const char *name, const char *ph, phx_kernel kern, bool
     ar.push(beta);
     void **args = ar.list();
     const uint32_t block[3] = {256, 1, 1}, grid[3] = {(uint32_t)(M / 128), (uint32_t)(N / 128), 1};
+    // the split plans' partial sums: a buffer this host owns, bound to its
+    // stream, enough for the largest split the search tries
+    Workspace ws(cx.stream, (size_t)PHX_SPLIT_CHUNKS_MAX * M * N * 4);
     Tuner t{kern, {M, N, K},
             [&] {  // C starts at zero on every launch (main.rs:511)
                 check(phx_memset_async(cd.ptr, 0, M * N * esz, cx.stream), "memset");
@@ -639,6 +654,7 @@ void bench_flash(Ctx &cx, const char *name, const char *ph, phx_kernel kern, boo
     void **args = ar.list();
     // @launch(128) and Nq / BR blocks with BR = 128 (main.rs:974-981)
     const uint32_t block[3] = {128, 1, 1}, grid[3] = {(uint32_t)(Nq / 128), 1, 1};
+    Workspace ws(cx.stream, (size_t)PHX_SPLIT_CHUNKS_MAX * Nq * (D + 2) * 4);
     Tuner t{kern, {Nq, Nk, D},
             [&] {
                 check(phx_launch_by_name(ph, "flash_attention", grid, block, cx.stream, args),

@@ -117,6 +117,8 @@ def lib():
     L.phx_stream_create.argtypes = [ctypes.POINTER(_vp)]
     L.phx_stream_destroy.argtypes = [_vp]
     L.phx_stream_synchronize.argtypes = [_vp]
+    L.phx_stream_set_workspace.argtypes = [_vp, _u64, _sz]
+    L.phx_stream_get_workspace.argtypes = [_vp, ctypes.POINTER(_u64), ctypes.POINTER(_sz)]
     L.phx_event_create.argtypes = [ctypes.POINTER(_vp)]
     L.phx_event_destroy.argtypes = [_vp]
     L.phx_event_record.argtypes = [_vp, _vp]
@@ -166,6 +168,7 @@ def lib():
                                  ctypes.POINTER(ctypes.c_float)]
     L.phx_pod_create.argtypes = [ctypes.POINTER(_vp), _sz, ctypes.c_int]
     L.phx_pod_destroy.argtypes = [_vp]
+    L.phx_pod_get_arena.argtypes = [_vp, ctypes.POINTER(_vp)]
     L.phx_pod_set_tensor.argtypes = [_vp, ctypes.c_uint32, ctypes.c_char_p,
                                      ctypes.POINTER(_u64), ctypes.c_uint32]
     L.phx_pod_set_kernel.argtypes = [_vp, ctypes.c_uint32, ctypes.c_int]
@@ -268,6 +271,9 @@ class Stream:
     def destroy(self):
         if self.handle:
             check(lib().phx_stream_destroy(self.handle))
+            buf = _WORKSPACES.pop(self.handle, None)
+            if buf is not None:
+                buf.free()  # the stream was drained by its destroy
             self.handle = None
 
 
@@ -302,6 +308,41 @@ class Event:
 
 def _sh(stream):
     return stream.handle if isinstance(stream, Stream) else stream
+
+
+# Workspaces bound by bind_workspace, kept alive while bound: stream handle -> buffer
+_WORKSPACES = {}
+
+
+def set_workspace(stream, addr, nbytes):
+    """phx_stream_set_workspace: bind caller-owned device memory (256-byte
+    aligned) as the split workspace of launches on stream (None: the legacy
+    default stream); addr 0 unbinds.  The caller keeps the memory alive."""
+    check(lib().phx_stream_set_workspace(_sh(stream), int(addr), int(nbytes)))
+
+
+def get_workspace(stream):
+    """(address, bytes) of the workspace bound to stream, (0, 0) for none."""
+    a, n = _u64(), _sz()
+    check(lib().phx_stream_get_workspace(_sh(stream), ctypes.byref(a), ctypes.byref(n)))
+    return a.value, n.value
+
+
+def bind_workspace(stream, nbytes):
+    """Allocates a workspace of nbytes (hipMalloc, 256-byte aligned) and binds
+    it to stream, replacing (and freeing) one an earlier call bound; nbytes 0
+    unbinds.  Split launches on the stream then use it; the launches
+    themselves never allocate."""
+    key = _sh(stream)
+    set_workspace(stream, 0, 0)
+    old = _WORKSPACES.pop(key, None)
+    if old is not None:
+        synchronize()  # launches in flight may still use it
+        old.free()
+    if nbytes:
+        buf = DeviceBuffer(nbytes)
+        set_workspace(stream, buf.ptr, nbytes)
+        _WORKSPACES[key] = buf
 
 
 # ------------------------------------------------------------------- launches

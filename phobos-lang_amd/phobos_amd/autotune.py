@@ -26,8 +26,8 @@ import math
 import numpy as np
 
 from . import (FLASH_FP16, FLASH_FP16_BH, FLASH_FP32_BH, GEMM_FP16, GEMM_FP16TC_FP32ACC,
-               DeviceBuffer, Event, PhxError, launch_flash, launch_flash_bh,
-               launch_gemm, normal_f32, plan_pin, to_f16_bits)
+               DeviceBuffer, Event, PhxError, bind_workspace, get_workspace, launch_flash,
+               launch_flash_bh, launch_gemm, normal_f32, plan_pin, to_f16_bits)
 
 SPLITS = (1, 2, 3, 4, 6, 8, 12, 16)  # the split counts a search tries
 MAX_WORKSPACE = 4 << 30               # skip splits whose partial sums need more
@@ -142,6 +142,15 @@ class Autotuner:
                             "spread_us": (f["max"] - f["min"]) * 1e6} for f in fin]}
 
 
+def ensure_workspace(stream, nbytes):
+    """Split launches take their partial results from the workspace bound to
+    their stream and run unsplit without one; the search binds one large
+    enough for every plan it times (replacing a smaller one), and the winner
+    then runs with it."""
+    if get_workspace(stream)[1] < nbytes:
+        bind_workspace(stream, nbytes)
+
+
 def _close(got, want, tol):
     got = np.asarray(got, np.float64)
     want = np.asarray(want, np.float64)
@@ -187,8 +196,10 @@ def tune_gemm(stream, kernel, M, N, K, alpha=1.0, beta=0.0, seed=1, **kw):
         _close(result(), want, tol)
 
     reset = None if beta == 0.0 else (lambda: C.upload(c0))
+    space = gemm_space(kernel, M, N, K)
+    ensure_workspace(stream, max(sp for sp, _ in space) * M * N * 4)
     tuner = Autotuner(stream, kernel, dims, run_once, verify, reset=reset, **kw)
-    return tuner.run(gemm_space(kernel, M, N, K))
+    return tuner.run(space)
 
 
 def tune_flash(stream, kernel, BH, Nq, Nk, D=64, scale=0.125, seed=1, **kw):
@@ -225,6 +236,8 @@ def tune_flash(stream, kernel, BH, Nq, Nk, D=64, scale=0.125, seed=1, **kw):
     def verify():
         _close(result(), want, tol)
 
+    space = flash_space(BH, Nq, Nk)
+    ensure_workspace(stream, max(sp for sp, _ in space) * BH * Nq * (D + 2) * 4)
     tuner = Autotuner(stream, kernel, dims, launch, verify, **kw)
-    return tuner.run(flash_space(BH, Nq, Nk))
+    return tuner.run(space)
 

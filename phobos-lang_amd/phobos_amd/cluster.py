@@ -296,6 +296,14 @@ class Pod:
         check(lib().phx_pod_run_segment(self.h, text.encode(), st))
         return dict(zip(STATS, list(st)))
 
+    def arena_stats(self):
+        """(capacity, bump offset, base address) of the pod's device arena."""
+        a = ctypes.c_void_p()
+        check(lib().phx_pod_get_arena(self.h, ctypes.byref(a)))
+        cap, bump, base = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_uint64()
+        check(lib().phx_arena_stats(a, ctypes.byref(cap), ctypes.byref(bump), ctypes.byref(base)))
+        return cap.value, bump.value, base.value
+
     def set_manifest_pb(self, data):
         """Applies an encoded phobos.v1.JobManifest (tensors, kernels)."""
         check(lib().phx_pod_set_manifest_pb(self.h, data, len(data)))

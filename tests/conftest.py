@@ -22,6 +22,13 @@ def px_gpu():
     return px
 
 
+# Split workspace bound to the session stream: enough for every split the
+# GPU tests run or pin (16 K chunks of a 2048 x 2048 f32 output at most).
+STREAM_WORKSPACE = 256 << 20
+
+
 @pytest.fixture(scope="session")
 def stream(px_gpu):
-    return px_gpu.Stream()
+    s = px_gpu.Stream()
+    px_gpu.bind_workspace(s, STREAM_WORKSPACE)
+    return s

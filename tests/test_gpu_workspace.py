@@ -1,0 +1,233 @@
+"""Split launches draw their workspace from memory the caller owns.
+
+The reference's kernels never allocate: every buffer a launch touches is the
+caller's (phobos-bench's DeviceBuffers; a pod COMPUTE touches only arena
+tiles, phobos-pod/src/tile_store.rs:14-83, engine.rs:582-647).  This
+backend splits small launches over K or over the keys; the split's partial
+results go to the workspace bound to the launch stream
+(phx_stream_set_workspace), or, in a pod, to an arena slab.  Checked here:
+
+  * the reference bench's own one-head 4096 x 4096 flash launch
+    (phx_launch_by_name with the .ph geometry, main.rs:334-371) and a 512^3
+    gemm_fp32 through phx_compute run split inside the bound workspace (its
+    sentinel bytes are overwritten), leave hipMemGetInfo's free bytes
+    unchanged, and meet the oracle;
+  * the same launches on a stream with no workspace run unsplit, allocate
+    nothing and meet the oracle; with a workspace too small for the built-in
+    plan they take fewer chunks;
+  * a pod's split COMPUTE takes its slab through the arena (the bump pointer
+    moves past the tiles) and leaves device memory unchanged.
+"""
+import ctypes
+import gc
+
+import numpy as np
+import pytest
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+SENTINEL = 0x7F  # 0x7F7F7F7F: a large finite f32 no partial result equals
+
+
+class _NoGc:
+    """Collects garbage first and holds the cyclic collector off, so no
+    buffer of an earlier test is freed while free memory is compared."""
+
+    def __enter__(self):
+        gc.collect()
+        gc.disable()
+
+    def __exit__(self, *exc):
+        gc.enable()
+
+
+def _free_bytes():
+    hip = ctypes.CDLL("libamdhip64.so")
+    free, total = ctypes.c_size_t(), ctypes.c_size_t()
+    assert hip.hipMemGetInfo(ctypes.byref(free), ctypes.byref(total)) == 0
+    return free.value
+
+
+def _flash_args(px, dq, dk, dv, do, Nq, Nk, D, scale):
+    """The launch! argument list of flash_attention_fp16.ph: four i64
+    exploded memrefs and the f32 scale (main.rs:352-367)."""
+    vals = []
+    for buf, n in ((dq, Nq), (dk, Nk), (dv, Nk), (do, Nq)):
+        vals += [ctypes.c_uint64(buf.ptr), ctypes.c_uint64(buf.ptr), ctypes.c_int64(0),
+                 ctypes.c_int64(n), ctypes.c_int64(D), ctypes.c_int64(D), ctypes.c_int64(1)]
+    vals.append(ctypes.c_float(scale))
+    arr = (ctypes.c_void_p * len(vals))(*[ctypes.cast(ctypes.byref(v), ctypes.c_void_p)
+                                         for v in vals])
+    return vals, arr
+
+
+def _one_head_flash(px, stream, Nq=4096, Nk=4096, D=64, scale=0.125, seed=5):
+    q, k, v = (oracle.f16_bits(oracle.normal_f32(seed + i, n * D)) for i, n in
+               enumerate((Nq, Nk, Nk)))
+    dq, dk, dv = (px.DeviceBuffer.from_array(t) for t in (q, k, v))
+    do = px.DeviceBuffer(Nq * D * 2)
+    keep, args = _flash_args(px, dq, dk, dv, do, Nq, Nk, D, scale)
+    grid = (ctypes.c_uint32 * 3)(Nq // 128, 1, 1)  # @launch(128), BR = 128
+    block = (ctypes.c_uint32 * 3)(128, 1, 1)
+
+    def launch():
+        px.check(px.lib().phx_launch_by_name(b"flash_attention_fp16", b"flash_attention", grid,
+                                             block, px._sh(stream), args))
+
+    def check():
+        got = oracle.f16_to_f32(do.download(np.uint16, Nq * D)).reshape(Nq, D)
+        rows = np.array([0, 1, Nq // 2, Nq - 1])
+        qq, kk, vv = (oracle.f16_to_f32(t) for t in (q, k, v))
+        want = oracle.flash_rows(rows, qq.reshape(Nq, D), kk.reshape(Nk, D), vv.reshape(Nk, D),
+                                 scale)
+        err = (np.abs(got[rows] - want) / np.maximum(np.abs(want), 0.1)).max()
+        assert err < 2e-2, err
+        assert np.isfinite(got).all()
+        return got
+
+    return launch, check, (dq, dk, dv, do, keep)
+
+
+def _gemm_fp32_compute(px, stream, M=512, N=512, K=512, alpha=0.125, beta=1.5, seed=11):
+    a, b, c = (oracle.lcg_f32(seed + i, n) for i, n in enumerate((M * K, K * N, M * N)))
+    da, db, dc = (px.DeviceBuffer.from_array(t) for t in (a, b, c))
+    fn = px.builtin_function(px.GEMM_FP32)
+    want = oracle.gemm_full(a.reshape(M, K), b.reshape(K, N), c.reshape(M, N), alpha, beta)
+
+    def launch():
+        dc.upload(c)
+        px.compute(fn, 32, [(da.ptr, (M, K)), (db.ptr, (K, N)), (dc.ptr, (M, N))],
+                   [(3, 4, px.f32_bits(alpha)), (4, 4, px.f32_bits(beta))],
+                   (M // 128, N // 128, 1), (256, 1, 1), stream)
+
+    def check():
+        got = dc.download(np.float32, M * N).reshape(M, N)
+        rel = np.abs(got - want) / np.maximum(np.abs(want), 1e-2 * np.sqrt(np.mean(want ** 2)))
+        assert rel.max() < 1e-4, rel.max()
+
+    return launch, check, (da, db, dc)
+
+
+def _run_checked(px, stream, launch, check, ws=None):
+    """Warm launch (a first launch loads the code object, which allocates),
+    then a launch bracketed by hipMemGetInfo.  With ws (a DeviceBuffer bound
+    as the workspace) filled with the sentinel, returns whether the launch
+    wrote into it."""
+    launch()
+    stream.synchronize()
+    if ws is not None:
+        px.check(px.lib().phx_memset_async(ws.ptr, SENTINEL, ws.nbytes, None))
+        px.synchronize()
+    with _NoGc():
+        before = _free_bytes()
+        launch()
+        stream.synchronize()
+        after = _free_bytes()
+    assert after == before, f"the launch changed free device memory by {before - after} B"
+    check()
+    if ws is not None:
+        w = ws.download(np.uint8, ws.nbytes)
+        return bool((w != SENTINEL).any())
+    return False
+
+
+@pytest.fixture()
+def bare_stream(px_gpu):
+    s = px_gpu.Stream()
+    yield s
+    s.destroy()
+
+
+def test_reference_flash_launch_splits_inside_the_bound_workspace(px_gpu, bare_stream):
+    px, s = px_gpu, bare_stream
+    sp, need = px.split_plan(px.FLASH_FP16, [4096, 4096, 64])
+    assert sp > 1 and need > 0
+    ws = px.DeviceBuffer(need)
+    px.set_workspace(s, ws.ptr, need)
+    assert px.get_workspace(s) == (ws.ptr, need)
+    launch, check, _ = _one_head_flash(px, s)
+    assert _run_checked(px, s, launch, check, ws), "the split did not use the bound workspace"
+    px.set_workspace(s, 0, 0)
+    assert px.get_workspace(s) == (0, 0)
+
+
+def test_unbound_stream_runs_unsplit_and_allocates_nothing(px_gpu, bare_stream):
+    px, s = px_gpu, bare_stream
+    assert px.get_workspace(s) == (0, 0)
+    launch, check, _ = _one_head_flash(px, s, seed=15)
+    _run_checked(px, s, launch, check)
+    glaunch, gcheck, _ = _gemm_fp32_compute(px, s, seed=21)
+    _run_checked(px, s, glaunch, gcheck)
+
+
+def test_gemm_compute_splits_inside_the_bound_workspace(px_gpu, bare_stream):
+    px, s = px_gpu, bare_stream
+    sp, need = px.split_plan(px.GEMM_FP32, [512, 512, 512])
+    assert sp > 1 and need == sp * 512 * 512 * 4
+    ws = px.DeviceBuffer(need)
+    px.set_workspace(s, ws.ptr, need)
+    launch, check, _ = _gemm_fp32_compute(px, s)
+    assert _run_checked(px, s, launch, check, ws)
+    # a workspace that holds three chunks: the launch takes at most three
+    small = 3 * 512 * 512 * 4
+    px.set_workspace(s, ws.ptr, small)
+    px.check(px.lib().phx_memset_async(ws.ptr, SENTINEL, need, None))
+    px.synchronize()
+    launch()
+    s.synchronize()
+    check()
+    w = ws.download(np.uint8, need)
+    assert (w[:small] != SENTINEL).any() and (w[small:] == SENTINEL).all()
+    px.set_workspace(s, 0, 0)
+
+
+def test_misaligned_workspace_is_refused(px_gpu, bare_stream):
+    px = px_gpu
+    with pytest.raises(px.PhxError, match="256-byte"):
+        px.set_workspace(bare_stream, 0x1000 + 16, 1 << 20)
+
+
+def test_pod_split_compute_takes_an_arena_slab(px_gpu, tmp_path):
+    # A 512^3 gemm_fp32 COMPUTE (split 16 ways by the built-in rule) in a
+    # pod: the tiles take 3 MiB of the arena and the split's partial sums
+    # another 16 MiB slab while the leaf runs; free device memory is the
+    # same before and after the segment.  With an arena too small for the
+    # slab the leaf runs unsplit, to the same bound.
+    from phobos_amd import cluster as cl
+    px = px_gpu
+    M = N = K = 512
+    alpha, beta = 0.125, 1.5
+    sp, need = px.split_plan(px.GEMM_FP32, [M, N, K])
+    assert sp > 1
+    a, b, c = (oracle.lcg_f32(31 + i, n) for i, n in enumerate((M * K, K * N, M * N)))
+    want = oracle.gemm_full(a.reshape(M, K), b.reshape(K, N), c.reshape(M, N), alpha, beta)
+    paths = [str(tmp_path / f) for f in ("a.bin", "b.bin", "c.bin", "out.bin")]
+    for p, t in zip(paths, (a, b, c, c)):
+        t.tofile(p)
+    seg = "\n".join([
+        f"1 - ALLOC 1 {M}x{K} f32", f"2 - ALLOC 2 {K}x{N} f32", f"3 - ALLOC 3 {M}x{N} f32",
+        f"4 1 LOAD 1 0 0,0 {M},{K}", f"5 2 LOAD 2 1 0,0 {K},{N}", f"6 3 LOAD 3 2 0,0 {M},{N}",
+        f"7 4,5,6 COMPUTE 1 1:r,2:r,3:rmw 3:f32:0x{px.f32_bits(alpha):08x},"
+        f"4:f32:0x{px.f32_bits(beta):08x} 4,4,1 256,1,1",
+        f"8 7 STORE 3 3 0,0 {M},{N}",
+        "9 8 FREE 1 0", "10 8 FREE 2 0", "11 8 FREE 3 0"]) + "\n"
+    tiles = 4 * (M * K + K * N + M * N)
+    for arena, split in ((tiles + need + (1 << 20), True), (tiles + (1 << 20), False)):
+        pod = cl.Pod(arena, 2)
+        for t, (p, shape) in enumerate(zip(paths, ((M, K), (K, N), (M, N), (M, N)))):
+            pod.set_tensor(t, "file://" + p, shape)
+        pod.set_kernel(1, px.GEMM_FP32)
+        pod.run(seg)  # warm: code objects, staging buffers
+        with _NoGc():
+            before = _free_bytes()
+            st = pod.run(seg)
+            assert _free_bytes() == before
+        assert st["compute"] == 1
+        bump = pod.arena_stats()[1]
+        assert (bump >= tiles + need) == split, (bump, tiles, need)
+        got = np.fromfile(paths[3], np.float32).reshape(M, N)
+        rel = np.abs(got - want) / np.maximum(np.abs(want), 1e-2 * np.sqrt(np.mean(want ** 2)))
+        assert rel.max() < 1e-4, (split, rel.max())
+        pod.close()
