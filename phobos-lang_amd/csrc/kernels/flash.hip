@@ -314,20 +314,12 @@ __device__ __forceinline__ void pv(phx_f16v (&acc)[2], const char *Vs, const phx
     __builtin_amdgcn_sched_barrier(0);
 }
 
-// The sum of a packed f16 pair in f32, starting a dot2 chain: the VOP3 form
-// of v_dot2_f32_f16 with an inline-constant zero addend.  (From a zero
-// variable the compiler emits a v_mov of the zero plus the in-place v_dot2c.)
-__device__ __forceinline__ float dot2_first(phx_h2 pp) {
-    float r;
-    asm("v_dot2_f32_f16 %0, %1, %2, 0" : "=v"(r) : "v"(pp), "s"(0x3c003c00u));  // (1, 1)
-    return r;
-}
-
-// exp2(s*c2 - m2) as f16 MFMA operands pf[c] (keys 16c + ...), and the f32
-// sum of the f16 values (v_dot2_f32_f16 against (1, 1)).
+// exp2(s*c2 - m2) as f16 MFMA operands pf[c] (keys 16c + ...), and the sum
+// of the f32 p values before their rounding to f16, as the reference sums
+// l over the f32 P (examples/flash_attention_fp16.ph:37-38: s = exp(s -
+// mnew); l += rowsum(s); P is rounded to f16 only for P.V).
 __device__ __forceinline__ float softmax_p(phx_h8 (&pf)[4], const phx_f16v (&s)[2], float c2,
                                            float m2) {
-    const phx_h2 ones = {(_Float16)1.0f, (_Float16)1.0f};
     float part[4];  // one partial sum per key slice: four short dependency chains
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -336,8 +328,8 @@ __device__ __forceinline__ float softmax_p(phx_h8 (&pf)[4], const phx_f16v (&s)[
         for (int j = 0; j < 8; j += 2) {
             const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[c >> 1][8 * (c & 1) + j], c2, -m2));
             const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[c >> 1][8 * (c & 1) + j + 1], c2, -m2));
+            part[c] = j == 0 ? p0 + p1 : (part[c] + p0) + p1;
             const phx_h2 pp = {(_Float16)p0, (_Float16)p1};
-            part[c] = j == 0 ? dot2_first(pp) : __builtin_amdgcn_fdot2(pp, ones, part[c], false);
             v[j] = pp.x;
             v[j + 1] = pp.y;
         }

@@ -244,3 +244,40 @@ def test_raw_launch_refuses_inconsistent_descriptors(px_gpu, stream):
                                      stream.handle, args)
     assert rc == px.PHX_E_INVALID and "disagree" in px.lib().phx_last_error().decode()
     stream.synchronize()
+
+
+@pytest.mark.parametrize("split", ["1", "4"])
+def test_flash_fp16_row_sum_is_over_the_f32_p(px_gpu, stream, monkeypatch, split):
+    # flash_attention_fp16.ph:33-38: p = exp(s - mnew) is f32; l sums the
+    # f32 p, and only P.V sees p rounded to f16.  Known answer that tells the
+    # two apart: the first key of every 64-key block scores 1 (the row max,
+    # p = 1, in every block and so in every key chunk of a split launch),
+    # every other key scores b = f16(0.000616...), so with scale*log2e = 1
+    # each other p is 2^(b - 1) = 0.5 + 0.8747 * 2^-12, which f16 rounds down
+    # to 0.5.  With V = 1, O = sum f16(p) / sum p = (64 + 4032 * 0.5) /
+    # (64 + 4032 * p) = 0.999586, which rounds to the f16 1 - 2^-11.  A
+    # kernel that summed l over the f16-rounded p would return exactly 1.0.
+    px = px_gpu
+    monkeypatch.setenv("PHX_FLASH_SPLIT", split)
+    Nq, Nk, D = 64, 4096, 64
+    b = np.float16(0.000616)
+    scale = np.float32(1 / 1.4426950408889634)
+    assert np.float32(scale * np.float32(1.4426950408889634)) == 1.0
+    q = np.zeros((Nq, D), np.float32)
+    q[:, 0] = 1.0
+    k = np.zeros((Nk, D), np.float32)
+    k[:, 0] = float(b)
+    k[::64, 0] = 1.0
+    v = np.ones((Nk, D), np.float32)
+    p = 2.0 ** (float(b) - 1.0)
+    assert 0.87 < (p - 0.5) / 2 ** -12 < 0.88 and np.float16(p) == 0.5
+    n1, nb = Nk // 64, Nk - Nk // 64
+    want = np.float16((n1 + nb * 0.5) / (n1 + nb * p))
+    assert want == np.float16(1 - 2 ** -11)
+    dq, dk, dv = (_upload(px, t, 16) for t in (q, k, v))
+    do = px.DeviceBuffer(Nq * D * 2)
+    assert px.split_plan(px.FLASH_FP16, [Nq, Nk, D])[0] == int(split)
+    px.launch_flash(stream, px.FLASH_FP16, dq.ptr, dk.ptr, dv.ptr, do.ptr, Nq, Nk, D, float(scale))
+    stream.synchronize()
+    got = do.download(np.uint16, Nq * D).view(np.float16)
+    assert (got == want).all(), np.unique(got)
