@@ -86,7 +86,8 @@ def parse():
                          + ", ".join(BENCHES))
     ap.add_argument("--autotune", default=None, metavar="SPEC",
                     help="pin the launch plan instead of searching it, as phobos-bench's "
-                         "--autotune pins its tile dims (needs --bench): \"splits=N variant=V\"")
+                         "--autotune pins its tile dims (needs --bench): \"splits=N variant=V\", for "
+                         "gemm_fp32 also \"TILE_M=128 TILE_N=128 TILE_K=16\"")
     ap.add_argument("--no-autotune", action="store_true",
                     help="skip the launch-plan search and use the runtime's built-in plans")
     ap.add_argument("--shapes", action="store_true",
@@ -107,10 +108,12 @@ def parse():
             name, eq, val = tok.partition("=")
             if not eq:
                 ap.error(f"bad autotune pin '{tok}', expected NAME=VALUE")
-            if name not in ("splits", "variant"):
+            dims = ("splits", "variant") + (("TILE_M", "TILE_N", "TILE_K")
+                                            if args.bench == "gemm_fp32" else ())
+            if name not in dims:
                 # autotune.rs:42-51
                 ap.error(f"autotune pin '{name}' is not a search dim of this kernel "
-                         "(dims: splits, variant)")
+                         f"(dims: {', '.join(dims)})")
             try:
                 args.pins[name] = int(val)
             except ValueError:
@@ -303,8 +306,10 @@ def autotune_leg(px, stream, wanted, pins):
         kind, kid, dims, kw = jobs[name]
         pdims = list(dims) + ([64] if kind == "flash" else [])
         if pins:
-            px.plan_pin(kid, pdims, pins.get("splits", 1), pins.get("variant", 0))
-            out[name] = {"pinned": list(px.plan_get(kid, pdims))}
+            plan = autotune.plan_from_pins(kid, pins)
+            px.plan_pin(kid, pdims, *plan)
+            out[name] = {"pinned": list(px.plan_get(kid, pdims)),
+                         "plan": autotune.plan_name(kid, plan)}
             continue
         t0 = time.perf_counter()
         try:
@@ -317,10 +322,11 @@ def autotune_leg(px, stream, wanted, pins):
             out[name] = {"error": str(e), "plan": list(px.plan_get(kid, pdims))}
             log(f"autotune {name} failed ({e}); built-in plan {out[name]['plan']}")
             continue
-        out[name] = {"winner": list(r["winner"]), "us": round(r["us"], 2),
+        out[name] = {"winner": list(r["winner"]), "plan": autotune.plan_name(kid, r["winner"]),
+                     "us": round(r["us"], 2),
                      "finalists": [[list(f["plan"]), round(f["us"], 2)] for f in r["stage2"]],
                      "plans_tried": len(r["stage1"]), "s": round(time.perf_counter() - t0, 2)}
-        log(f"autotune {name}: winner (splits, variant) = {r['winner']}, {r['us']:.1f} us; "
+        log(f"autotune {name}: winner {out[name]['plan']}, {r['us']:.1f} us; "
             f"finalists {out[name]['finalists']}")
     return out
 

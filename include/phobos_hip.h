@@ -182,7 +182,13 @@ int phx_split_plan(phx_kernel k, const int64_t *dims, int ndims, int *splits,
  * kernels); here each kernel has one tile shape and these are its choices:
  *   splits   K chunks (gemm_fp32, gemm_fp16tc_fp32acc, gemm_fp16) or key
  *            chunks (flash), 1 .. 16, 1 for none;
- *   variant  gemm_fp16tc_fp32acc on whole 256 x 256 tiles: 0 the eight-wave
+ *   variant  gemm_fp32: the tiling TILE_M x TILE_N x TILE_K (the .ph file's
+ *            @autotune dims, examples/gemm_fp32.ph:1): 0 256x256x16 (the
+ *            built-in tiling, the only one that splits), 1 256x128x16,
+ *            2 128x256x16, 3 128x128x16, 4 128x128x32, 5 128x128x8,
+ *            6 256x256x8, 7 64x64x16 (code object entries "gemm" and
+ *            "gemm_t<M>x<N>k<K>");
+ *            gemm_fp16tc_fp32acc on whole 256 x 256 tiles: 0 the eight-wave
  *            kernel, 1 the one-wave kernel; 0 for every other kernel.
  * A launch uses the plan pinned for its kernel and dims, else the built-in
  * rule.  The PHX_GEMM_SPLIT, PHX_FLASH_SPLIT and PHX_GEMM_W8 environment
@@ -196,7 +202,8 @@ int phx_plan_get(phx_kernel k, const int64_t *dims, int ndims, phx_plan *plan);
 /* Pins plan for k at dims (plan NULL removes the pin).  The one-head and
  * batched flash kernels of a precision share pins, the one-head dims meaning
  * one head.  PHX_E_INVALID for a kernel without choices, splits outside
- * 1 .. 16 or a variant the kernel lacks. */
+ * 1 .. 16, a variant the kernel lacks, or a gemm_fp32 tiling other than 0
+ * with splits above 1. */
 int phx_plan_pin(phx_kernel k, const int64_t *dims, int ndims, const phx_plan *plan);
 /* Removes every pin. */
 int phx_plan_unpin_all(void);

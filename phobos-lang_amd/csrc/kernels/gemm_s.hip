@@ -47,23 +47,10 @@
 //   * Workgroups are renumbered XCD-major and grouped 4 tile-rows deep.
 #include "phx_common.h"
 
-#define BM PHX_S_TILE
-#define BN PHX_S_TILE
-#define BK PHX_S_BK
 #define NT PHX_S_THREADS
-#define WM 128
-#define WN 128
 #define GROUP_M 4
-
-#define A_ROW_BYTES (BK * 4)             // 64
-#define B_ROW_BYTES (BN * 4)             // 1024
-#define A_BYTES (BM * A_ROW_BYTES)       // 16 KiB
-#define B_BYTES (BK * B_ROW_BYTES)       // 16 KiB
-#define STAGE_BYTES (A_BYTES + B_BYTES)  // 32 KiB
 #define NSTG 3
-#define DMA_PER_STEP 8                   // copies per wave per K step (4 A + 4 B)
-#define EP_RP 8                          // epilogue rows per pass
-#define EP_PITCH 136                     // epilogue LDS row pitch (floats)
+#define EP_RP 8  // epilogue rows per pass
 
 typedef __attribute__((address_space(3))) void *phx_lds_vp;
 
@@ -74,151 +61,240 @@ typedef __attribute__((address_space(3))) void *phx_lds_vp;
 #define G_VMEM 0x020
 #define G_DSR 0x100
 
-__device__ __forceinline__ uint32_t a_off(uint32_t row, uint32_t chunk) {
-    return row * A_ROW_BYTES + ((chunk ^ ((row >> 2) & 3)) << 4);
-}
-__device__ __forceinline__ uint32_t b_off(uint32_t row, uint32_t chunk) {
-    return row * B_ROW_BYTES + ((chunk ^ (((row >> 2) & 1) << 3)) << 4);
-}
-
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t phx_rsrc(const void *p, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes,
                                              0x00020000);
 }
 
-// Operands of k-group q (k = 8q .. 8q+7) for this wave: a[i] = A row wm +
-// 32i + lane%32, k = 8q + 4g .. +3; b[j][s] = B[8q + 4g + s][wn + 32j + lane%32].
-struct Frags {
-    phx_f4 a[4];
-    float b[4][4];
+// One tiling: a TM x TN output tile per workgroup of 4 waves in a 2 x 2
+// arrangement (each WM x WN = MI x NJ MFMA tiles of 32 x 32), K steps of TK.
+// TK = 8, 16 or 32 (1, 2 or 4 k-groups of 8 per step); TM, TN multiples of
+// 64.  The tilings the reference's autotuner chooses among are its
+// @autotune(TILE_M, TILE_N in [32, 256], TILE_K in [4, 32]) dims
+// (examples/gemm_fp32.ph:1); the built-in plan is 256 x 256 x 16.
+template <int TM_, int TN_, int TK_>
+struct Tile {
+    static constexpr int TM = TM_, TN = TN_, TK = TK_;
+    static constexpr int WM = TM / 2, WN = TN / 2;
+    static constexpr int MI = WM / 32, NJ = WN / 32;
+    static constexpr int CA = TK / 4;    // 16-byte chunks per A row
+    static constexpr int RA = 64 / TK;   // A rows per 256 bytes (one LDS bank sweep)
+    static constexpr int NQ = TK / 8;    // k-groups per step
+    static constexpr int A_BYTES = TM * TK * 4;
+    static constexpr int B_ROW = TN * 4;
+    static constexpr int B_BYTES = TK * B_ROW;
+    static constexpr int STAGE = A_BYTES + B_BYTES;
+    static constexpr int A_COPIES = A_BYTES / 4096;  // 1 KiB copies per wave per step
+    static constexpr int B_COPIES = B_BYTES / 4096;
+    static constexpr int DMA = A_COPIES + B_COPIES;
+    static constexpr int A_RPC = 64 / CA;      // A rows per copy
+    static constexpr int B_LPR = TN / 4;       // lanes per B row in a copy
+    static constexpr int B_RPC = 64 / B_LPR;   // B rows per copy
+    static constexpr int NMF = 4 * MI * NJ;    // MFMAs per k-group
+    static constexpr int RD = MI + 4 * NJ;     // LDS operand reads per k-group
+    static constexpr int EP_PITCH = WN + 8;    // epilogue LDS row pitch (floats)
+    static constexpr int EP_LPR = WN / 4;      // lanes per epilogue row
+    static constexpr int EP_RPI = 64 / EP_LPR; // rows per epilogue store
+    static constexpr int OCC = MI * NJ * 16 <= 128 ? 2 : 1;  // workgroups per CU
+    static_assert(TK == 8 || TK == 16 || TK == 32, "TK");
+    static_assert(TM % 64 == 0 && TN % 64 == 0 && TN <= 256, "TM, TN");
+    static_assert(A_COPIES >= 1 && B_COPIES >= 1 && A_BYTES % 4096 == 0 && B_BYTES % 4096 == 0,
+                  "whole copies per wave");
+    static_assert(CA < 8 || A_COPIES % 2 == 0, "TK = 32: A copies come in pairs");
+    static_assert(4 * EP_RP * EP_PITCH * 4 <= NSTG * STAGE, "epilogue fits in the stages");
 };
 
-__device__ __forceinline__ void read_frags(Frags &f, const char *stage, uint32_t q, uint32_t wm,
-                                           uint32_t wn, uint32_t lane) {
-    const char *As = stage, *Bs = stage + A_BYTES;
+// A is staged As[m][k] (TK*4-byte rows) with 16-byte chunks XOR ((row / RA) &
+// (CA - 1)), so the 16 rows one ds_read_b128 quarter-wave reads at one
+// logical chunk land in 16 distinct 16-byte slots of the 256-byte bank sweep.
+template <class T>
+__device__ __forceinline__ uint32_t a_off(uint32_t row, uint32_t chunk) {
+    return row * (T::TK * 4) + ((chunk ^ ((row / T::RA) & (T::CA - 1))) << 4);
+}
+// B stays row-major Bs[k][n]; rows whose k differs by 4 (the two lane groups
+// of an operand read) are offset by 128 bytes.
+template <class T>
+__device__ __forceinline__ uint32_t b_off(uint32_t row, uint32_t chunk) {
+    return row * T::B_ROW + ((chunk ^ (((row >> 2) & 1) << 3)) << 4);
+}
+
+// Operands of k-group q (k = 8q .. 8q+7) for this wave: a[i] = A row wm +
+// 32i + lane%32, k = 8q + 4g .. +3; b[j][s] = B[8q + 4g + s][wn + 32j + lane%32].
+template <class T>
+struct Frags {
+    phx_f4 a[T::MI];
+    float b[T::NJ][4];
+};
+
+template <class T>
+__device__ __forceinline__ void read_frags(Frags<T> &f, const char *stage, uint32_t q,
+                                           uint32_t wm, uint32_t wn, uint32_t lane) {
+    const char *As = stage, *Bs = stage + T::A_BYTES;
     const uint32_t lrow = lane & 31, g = lane >> 5;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-        f.a[i] = *(const phx_f4 *)(As + a_off(wm + 32 * i + lrow, 2 * q + g));
+    for (int i = 0; i < T::MI; ++i)
+        f.a[i] = *(const phx_f4 *)(As + a_off<T>(wm + 32 * i + lrow, 2 * q + g));
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < T::NJ; ++j)
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             const uint32_t row = 8 * q + 4 * g + s, col = wn + 32 * j + lrow;
-            f.b[j][s] = *(const float *)(Bs + b_off(row, col >> 2) + 4 * (col & 3));
+            f.b[j][s] = *(const float *)(Bs + b_off<T>(row, col >> 2) + 4 * (col & 3));
         }
 }
 
-// MFMA order: s outermost, then (i, j): 16 independent accumulators between
-// two updates of the same one.
-__device__ __forceinline__ void mfma_all(phx_f16v (&acc)[4][4], const Frags &f) {
+// MFMA order: s outermost, then (i, j): MI*NJ independent accumulators
+// between two updates of the same one.
+template <class T>
+__device__ __forceinline__ void mfma_all(phx_f16v (&acc)[T::MI][T::NJ], const Frags<T> &f) {
 #pragma unroll
     for (int s = 0; s < 4; ++s)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < T::MI; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < T::NJ; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(f.a[i][s], f.b[j][s], acc[i][j],
                                                                  0, 0, 0);
 }
 
-// Copies K step k0 of A and B into stage dst.  A: copy i of wave w covers
-// rows 64w + 16i + lane/4 (lane's physical chunk lane%4); B: copy i covers
-// row 4w + i (lane's physical chunk = lane).  Each lane fetches the logical
-// chunk its swizzled slot holds.  Rows past M read zeros.
+// Copies K step k0 of A and B into stage dst.  Copy c of the workgroup (c =
+// wave * COPIES + i) fills 1 KiB of LDS, lane l the l-th 16-byte slot: for A
+// rows c*A_RPC + l/CA, physical chunk l%CA; for B rows c*B_RPC + l/B_LPR,
+// physical chunk l%B_LPR.  Each lane fetches the logical chunk its swizzled
+// slot holds.  Rows past M (A) and past K (B) read zeros through the
+// resource bounds; in the last, partial K step A chunks past K take an
+// out-of-range offset and read zeros.
+template <class T>
 __device__ __forceinline__ void dma_step(char *dst, const float *A, int64_t lda, const float *B,
                                          int64_t ldb, int64_t M, int64_t N, int64_t K, uint32_t m0,
-                                         uint32_t n0, uint32_t k0, uint32_t voa, uint32_t voa_t,
-                                         uint32_t vob0, uint32_t vob1, uint32_t wave) {
+                                         uint32_t n0, uint32_t k0, uint32_t wave, uint32_t lane) {
     const bool in = (int64_t)k0 < K;
-    const int64_t mrows = M - m0 < BM ? M - m0 : BM;
+    const int64_t mrows = M - m0 < T::TM ? M - m0 : T::TM;
     const int64_t kr = in ? K - k0 : 0;  // columns of this step that exist
-    const int64_t kw = kr < BK ? kr : BK;
+    const int64_t kw = kr < T::TK ? kr : T::TK;
     const __amdgpu_buffer_rsrc_t ra = phx_rsrc(
         A + (int64_t)m0 * lda + (in ? k0 : 0), in ? (uint32_t)(((mrows - 1) * lda + kw) * 4) : 0);
-    // the last, partial step uses the offsets that read zero past K
-    const uint32_t va = kw == BK ? voa : voa_t;
-    // B rows are full 1 KiB reads even when the tile crosses N: columns past
-    // N land in output columns that are not stored; the resource ends at the
+    // B rows are full reads even when the tile crosses N: columns past N land
+    // in output columns that are not stored; the resource ends at the
     // matrix's last element.
     const int64_t brem = (K - (in ? k0 : 0) - 1) * ldb + (N - n0);
-    const uint32_t bbytes = (uint32_t)((brem < (BK - 1) * ldb + BN ? brem : (BK - 1) * ldb + BN) * 4);
+    const int64_t bmax = (int64_t)(T::TK - 1) * ldb + T::TN;
+    const uint32_t bbytes = (uint32_t)((brem < bmax ? brem : bmax) * 4);
     const __amdgpu_buffer_rsrc_t rb =
         phx_rsrc(B + (int64_t)(in ? k0 : 0) * ldb + n0, in ? bbytes : 0);
+    const uint32_t ar = lane / T::CA, apc = lane % T::CA;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < T::A_COPIES; ++i) {
+        // copy c's first row is 4c row-sweeps in, so only 4c & (CA - 1)
+        // (0, or 4 for odd copies when CA = 8) enters the swizzle
+        const uint32_t x = (4 * i) & (T::CA - 1);
+        const uint32_t c = apc ^ ((x + ar / T::RA) & (T::CA - 1));
+        const uint32_t va = 4 * c < (uint32_t)kw ? (uint32_t)(ar * lda * 4 + c * 16) : 0x80000000u;
+        const uint32_t row0 = (wave * T::A_COPIES + i) * T::A_RPC;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            ra, (phx_lds_vp)(dst + (wave * 256 + i * 64) * 16), 16, va,
-            (int)((uint32_t)((wave * 64 + i * 16) * lda) * 4), 0, 0);
+            ra, (phx_lds_vp)(dst + (wave * T::A_COPIES + i) * 1024), 16, va,
+            (int)((uint32_t)(row0 * lda) * 4), 0, 0);
+    }
+    const uint32_t br = lane / T::B_LPR, bpc = lane % T::B_LPR;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < T::B_COPIES; ++i) {
+        const uint32_t row0 = (wave * T::B_COPIES + i) * T::B_RPC;
+        const uint32_t c = bpc ^ ((((row0 + br) >> 2) & 1) << 3);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rb, (phx_lds_vp)(dst + A_BYTES + (wave * 4 + i) * B_ROW_BYTES), 16,
-            ((wave * 4 + i) >> 2) & 1 ? vob1 : vob0, (int)((uint32_t)((wave * 4 + i) * ldb) * 4),
-            0, 0);
+            rb, (phx_lds_vp)(dst + T::A_BYTES + (wave * T::B_COPIES + i) * 1024), 16,
+            br * (uint32_t)ldb * 4 + c * 16, (int)((uint32_t)(row0 * ldb) * 4), 0, 0);
+    }
 }
 
-__device__ __forceinline__ void k_step(phx_f16v (&acc)[4][4], Frags &F0, Frags &F1, char *cur,
-                                       const char *nxt, const float *A, int64_t lda,
-                                       const float *B, int64_t ldb, int64_t M, int64_t N,
-                                       int64_t K, uint32_t m0, uint32_t n0, uint32_t kt,
-                                       uint32_t voa, uint32_t voa_t, uint32_t vob0, uint32_t vob1,
-                                       uint32_t wm,
-                                       uint32_t wn, uint32_t wave, uint32_t lane) {
-    read_frags(F1, cur, 1, wm, wn, lane);
-    mfma_all(acc, F0);
+// Interleave of one k-group's MFMAs with the operand reads for the next
+// group (and, in the step's last group, the copies of step kt+3).
+template <class T, bool COPIES>
+__device__ __forceinline__ void sched_group() {
 #pragma unroll
-    for (int i = 0; i < 64; ++i) {
+    for (int i = 0; i < T::NMF; ++i) {
         SGB(G_MFMA, 1);
-        if (i < 20) SGB(G_DSR, 1);
+        if (i < T::RD) SGB(G_DSR, 1);
+        if (COPIES && i >= T::RD && i < T::RD + T::DMA) SGB(G_VMEM, 1);
     }
-    __builtin_amdgcn_sched_barrier(0);
-    PHX_WAIT_VM_LGKM0((NSTG - 2) * DMA_PER_STEP);  // own copies of kt+1 landed, reads of cur done
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_sched_barrier(0);
-    read_frags(F0, nxt, 0, wm, wn, lane);
-    dma_step(cur, A, lda, B, ldb, M, N, K, m0, n0, (kt + NSTG) * BK, voa, voa_t, vob0, vob1, wave);
-    mfma_all(acc, F1);
-#pragma unroll
-    for (int i = 0; i < 64; ++i) {
-        SGB(G_MFMA, 1);
-        if (i < 20) SGB(G_DSR, 1);
-        if (i >= 20 && i < 28) SGB(G_VMEM, 1);
+    if constexpr (T::RD > T::NMF) SGB(G_DSR, T::RD - T::NMF);
+    if constexpr (COPIES && T::RD + T::DMA > T::NMF) {
+        constexpr int left = T::RD >= T::NMF ? T::DMA : T::RD + T::DMA - T::NMF;
+        SGB(G_VMEM, left);
     }
-    __builtin_amdgcn_sched_barrier(0);
 }
 
-// Epilogue: per wave, 16 passes of 8 rows x 128 columns through a private
+// One K step: each k-group's MFMAs run while the next group's operands are
+// read; before the last group, the wait for this wave's copies of step kt+1
+// and the barrier, after which the next step's group 0 is read and step
+// kt+3 is copied into the stage this step releases.  F0 holds group 0 on
+// entry; on exit it holds the next step's group 0.
+template <class T>
+__device__ __forceinline__ void k_step(phx_f16v (&acc)[T::MI][T::NJ], Frags<T> &F0,
+                                       Frags<T> &F1, char *cur, const char *nxt, const float *A,
+                                       int64_t lda, const float *B, int64_t ldb, int64_t M,
+                                       int64_t N, int64_t K, uint32_t m0, uint32_t n0,
+                                       uint32_t kt, uint32_t wm, uint32_t wn, uint32_t wave,
+                                       uint32_t lane) {
+#pragma unroll
+    for (int q = 0; q < T::NQ; ++q) {
+        Frags<T> &Fc = (q & 1) ? F1 : F0;  // this group's operands
+        Frags<T> &Fn = (q & 1) ? F0 : F1;  // the next group's
+        if (q < T::NQ - 1) {
+            read_frags<T>(Fn, cur, q + 1, wm, wn, lane);
+            mfma_all<T>(acc, Fc);
+            sched_group<T, false>();
+        } else {
+            __builtin_amdgcn_sched_barrier(0);
+            // own copies of kt+1 landed, reads of cur done
+            PHX_WAIT_VM_LGKM0((NSTG - 2) * T::DMA);
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+            read_frags<T>(Fn, nxt, 0, wm, wn, lane);
+            dma_step<T>(cur, A, lda, B, ldb, M, N, K, m0, n0, (kt + NSTG) * T::TK, wave, lane);
+            mfma_all<T>(acc, Fc);
+            sched_group<T, true>();
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (T::NQ & 1) {  // the next step's group 0 was read into F1
+        const Frags<T> t = F0;
+        F0 = F1;
+        F1 = t;
+    }
+}
+
+// Epilogue: per wave, passes of EP_RP rows x WN columns through a private
 // LDS region; a lane then moves 4 consecutive values of a row.  STEP: the
 // cluster step leaf (C += alpha*acc), else C = alpha*acc + beta*C (C not read
 // when beta == 0).
-template <bool STEP>
-__device__ __forceinline__ void epilogue(const phx_f16v (&acc)[4][4], float *ep_all, float *C,
-                                         int64_t ldc, int64_t M, int64_t N, uint32_t m0,
+template <class T, bool STEP>
+__device__ __forceinline__ void epilogue(const phx_f16v (&acc)[T::MI][T::NJ], float *ep_all,
+                                         float *C, int64_t ldc, int64_t M, int64_t N, uint32_t m0,
                                          uint32_t n0, uint32_t wm, uint32_t wn, float alpha,
                                          float beta, uint32_t wave, uint32_t lane) {
     const uint32_t lrow = lane & 31, lgrp = lane >> 5;
-    float *ep = ep_all + wave * (EP_RP * EP_PITCH);
+    float *ep = ep_all + wave * (EP_RP * T::EP_PITCH);
 #pragma unroll
-    for (int pass = 0; pass < WM / EP_RP; ++pass) {
+    for (int pass = 0; pass < T::WM / EP_RP; ++pass) {
         const int i = (pass * EP_RP) / 32;
         const int r0 = ((pass * EP_RP) % 32) / 2;
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < T::NJ; ++j)
 #pragma unroll
             for (int r = r0; r < r0 + EP_RP / 2; ++r)
-                ep[(8 * (r >> 2) + 4 * lgrp + (r & 3) - 2 * r0) * EP_PITCH + 32 * j + lrow] =
+                ep[(8 * (r >> 2) + 4 * lgrp + (r & 3) - 2 * r0) * T::EP_PITCH + 32 * j + lrow] =
                     alpha * acc[i][j][r];
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-        for (int rr = 0; rr < EP_RP / 2; ++rr) {
-            const uint32_t row = rr * 2 + (lane >> 5), c4 = (lane & 31) * 4;
+        for (int rr = 0; rr < EP_RP / T::EP_RPI; ++rr) {
+            const uint32_t row = rr * T::EP_RPI + lane / T::EP_LPR;
+            const uint32_t c4 = (lane % T::EP_LPR) * 4;
             const int64_t grow = (int64_t)m0 + wm + pass * EP_RP + row;
             const int64_t gcol = (int64_t)n0 + wn + c4;
             if (grow < M && gcol < N) {
-                const phx_f4 v = *(const phx_f4 *)(ep + row * EP_PITCH + c4);
+                const phx_f4 v = *(const phx_f4 *)(ep + row * T::EP_PITCH + c4);
                 float *dst = C + grow * ldc + gcol;
                 phx_f4 o = v;
                 if (STEP) {
@@ -238,32 +314,22 @@ __device__ __forceinline__ void epilogue(const phx_f16v (&acc)[4][4], float *ep_
 
 // Tiles t0, t0 + tstride, ... of C (the regular entries walk them with the
 // linear block id over the whole grid; the split-K entry with blockIdx.x).
-template <bool STEP>
+template <class T, bool STEP>
 __device__ __forceinline__ void gemm_s_body(const float *A, int64_t lda, const float *B,
                                             int64_t ldb, float *C, int64_t ldc, int64_t M,
                                             int64_t N, int64_t K, float alpha, float beta,
-                                            char *stg0, char *stg1, char *stg2, uint32_t t0,
-                                            uint32_t tstride) {
-    char *const S[NSTG] = {stg0, stg1, stg2};
+                                            char *stg, uint32_t t0, uint32_t tstride) {
+    char *const S[NSTG] = {stg, stg + T::STAGE, stg + 2 * T::STAGE};
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t wm = (wave >> 1) * WM;
-    const uint32_t wn = (wave & 1) * WN;
-    const uint32_t tiles_n = (uint32_t)((N + BN - 1) / BN);
-    const uint32_t tiles_m = (uint32_t)((M + BM - 1) / BM);
+    const uint32_t wm = (wave >> 1) * T::WM;
+    const uint32_t wn = (wave & 1) * T::WN;
+    const uint32_t tiles_n = (uint32_t)((N + T::TN - 1) / T::TN);
+    const uint32_t tiles_m = (uint32_t)((M + T::TM - 1) / T::TM);
     const uint32_t ntiles = tiles_m * tiles_n;
     const uint32_t nblk = tstride;
-    const uint32_t nk = (uint32_t)((K + BK - 1) / BK);
-    const uint32_t voa =
-        (uint32_t)(((lane >> 2) * lda + 4 * ((lane & 3) ^ ((lane >> 4) & 3))) * 4);
-    // lane's logical A chunk covers k = 4 * ((lane & 3) ^ ((lane >> 4) & 3)) .. +3;
-    // in the last, partial K step chunks past K read zero
-    const uint32_t kwl = (uint32_t)(K % BK);
-    const uint32_t voa_t =
-        kwl == 0 || 4 * ((lane & 3) ^ ((lane >> 4) & 3)) < kwl ? voa : 0x80000000u;
-    const uint32_t vob0 = lane * 16;
-    const uint32_t vob1 = (lane ^ 8) * 16;
+    const uint32_t nk = (uint32_t)((K + T::TK - 1) / T::TK);
 
     for (uint32_t t = t0; t < ntiles; t += nblk) {
         const uint32_t ts = nblk == ntiles ? phx_xcd_swizzle(t, ntiles) : t;
@@ -272,44 +338,45 @@ __device__ __forceinline__ void gemm_s_body(const float *A, int64_t lda, const f
         const uint32_t gm = (tiles_m - g0) < GROUP_M ? (tiles_m - g0) : GROUP_M;
         const uint32_t tm = g0 + (ts % gsz) % gm;
         const uint32_t tn = (ts % gsz) / gm;
-        const uint32_t m0 = tm * BM, n0 = tn * BN;
+        const uint32_t m0 = tm * T::TM, n0 = tn * T::TN;
 
-        phx_f16v acc[4][4];
+        phx_f16v acc[T::MI][T::NJ];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < T::MI; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < T::NJ; ++j)
                 acc[i][j] = (phx_f16v){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-        Frags F0, F1;
+        Frags<T> F0, F1;
 #pragma unroll
         for (int p = 0; p < NSTG; ++p)
-            dma_step(S[p], A, lda, B, ldb, M, N, K, m0, n0, p * BK, voa, voa_t, vob0, vob1, wave);
-        PHX_WAIT_VMCNT((NSTG - 1) * DMA_PER_STEP);
+            dma_step<T>(S[p], A, lda, B, ldb, M, N, K, m0, n0, p * T::TK, wave, lane);
+        PHX_WAIT_VMCNT((NSTG - 1) * T::DMA);
         __builtin_amdgcn_s_barrier();
-        read_frags(F0, stg0, 0, wm, wn, lane);
+        read_frags<T>(F0, S[0], 0, wm, wn, lane);
         uint32_t kt = 0;
         for (; kt + NSTG <= nk; kt += NSTG) {
 #pragma unroll
             for (int u = 0; u < NSTG; ++u)
-                k_step(acc, F0, F1, S[u], S[(u + 1) % NSTG], A, lda, B, ldb, M, N, K, m0, n0,
-                       kt + u, voa, voa_t, vob0, vob1, wm, wn, wave, lane);
+                k_step<T>(acc, F0, F1, S[u], S[(u + 1) % NSTG], A, lda, B, ldb, M, N, K, m0, n0,
+                          kt + u, wm, wn, wave, lane);
         }
 #pragma unroll
         for (int u = 0; u < NSTG - 1; ++u)
             if (kt + u < nk)
-                k_step(acc, F0, F1, S[u], S[(u + 1) % NSTG], A, lda, B, ldb, M, N, K, m0, n0,
-                       kt + u, voa, voa_t, vob0, vob1, wm, wn, wave, lane);
+                k_step<T>(acc, F0, F1, S[u], S[(u + 1) % NSTG], A, lda, B, ldb, M, N, K, m0, n0,
+                          kt + u, wm, wn, wave, lane);
         PHX_WAIT_VMCNT(0);
         __syncthreads();
-        epilogue<STEP>(acc, (float *)stg0, C, ldc, M, N, m0, n0, wm, wn, alpha, beta, wave, lane);
+        epilogue<T, STEP>(acc, (float *)stg, C, ldc, M, N, m0, n0, wm, wn, alpha, beta, wave,
+                          lane);
         __syncthreads();
     }
 }
 
-#define GEMM_S_PRELUDE                                                                        \
-    __shared__ __attribute__((aligned(16))) char stg0[STAGE_BYTES];                           \
-    __shared__ __attribute__((aligned(16))) char stg1[STAGE_BYTES];                           \
-    __shared__ __attribute__((aligned(16))) char stg2[STAGE_BYTES];                           \
+typedef Tile<PHX_S_TILE, PHX_S_TILE, PHX_S_BK> Base;  // 256 x 256 x 16
+
+#define GEMM_S_PRELUDE(T)                                                                     \
+    __shared__ __attribute__((aligned(16))) char stg[NSTG * T::STAGE];                        \
     const int64_t M = a_s0, K = a_s1, N = b_s1;                                               \
     if (blockDim.x != NT || N % PHX_S_NK_MULT || K % PHX_S_NK_MULT || M <= 0 || N <= 0 ||  \
         K <= 0 || b_s0 != K || c_s0 != M || c_s1 != N || a_st1 != 1 || b_st1 != 1 ||         \
@@ -322,10 +389,37 @@ extern "C" __global__ __launch_bounds__(NT, 1) void gemm(PHX_MEMREF2(float, a, i
                                                           PHX_MEMREF2(float, b, int32_t),
                                                           PHX_MEMREF2(float, c, int32_t),
                                                           float alpha, float beta) {
-    GEMM_S_PRELUDE
-    gemm_s_body<false>(a_ptr + a_off, a_st0, b_ptr + b_off, b_st0, c_ptr + c_off, c_st0, M, N, K,
-                       alpha, beta, stg0, stg1, stg2, phx_block_linear(), phx_block_count());
+    GEMM_S_PRELUDE(Base)
+    gemm_s_body<Base, false>(a_ptr + a_off, a_st0, b_ptr + b_off, b_st0, c_ptr + c_off, c_st0, M,
+                             N, K, alpha, beta, stg, phx_block_linear(), phx_block_count());
 }
+
+// The other tilings of the gemm_fp32 launch plan (phx_plan variant 1 ..):
+// entry gemm_t<TM>x<TN>k<TK>, the same parameters and arithmetic as "gemm"
+// over TM x TN tiles and K steps of TK.  Each output is the same f32 sum of
+// exact products in a different order only where TK differs (the k-groups
+// of 8 are summed in order in every tiling).
+// workgroups per CU a tiling's registers allow (Tile::OCC, without the
+// commas a template argument list would put into __launch_bounds__)
+#define GEMM_S_OCC(AREA) ((AREA) <= 128 * 256 ? 2 : 1)
+#define GEMM_S_VARIANT(VM, VN, VK)                                                            \
+    extern "C" __global__ __launch_bounds__(NT, GEMM_S_OCC(VM * VN)) void                    \
+        gemm_t##VM##x##VN##k##VK(PHX_MEMREF2(float, a, int32_t), PHX_MEMREF2(float, b, int32_t), \
+                                 PHX_MEMREF2(float, c, int32_t), float alpha, float beta) {   \
+        typedef Tile<VM, VN, VK> T;                                                           \
+        static_assert(T::OCC == GEMM_S_OCC(VM * VN), "occupancy");                            \
+        GEMM_S_PRELUDE(T)                                                                     \
+        gemm_s_body<T, false>(a_ptr + a_off, a_st0, b_ptr + b_off, b_st0, c_ptr + c_off,      \
+                              c_st0, M, N, K, alpha, beta, stg, phx_block_linear(),           \
+                              phx_block_count());                                             \
+    }
+GEMM_S_VARIANT(256, 128, 16)
+GEMM_S_VARIANT(128, 256, 16)
+GEMM_S_VARIANT(128, 128, 16)
+GEMM_S_VARIANT(128, 128, 32)
+GEMM_S_VARIANT(128, 128, 8)
+GEMM_S_VARIANT(256, 256, 8)
+GEMM_S_VARIANT(64, 64, 16)
 
 // Split-K for shapes with too few output tiles to fill the GPU (the host
 // picks the split; see phx_runtime.cpp).  Workgroup (x, y) computes tiles
@@ -338,14 +432,12 @@ extern "C" __global__ __launch_bounds__(NT, 1) void gemm_splitk(const float *A, 
                                                                  int64_t ldb, int64_t M,
                                                                  int64_t N, int64_t K,
                                                                  int64_t kchunk) {
-    __shared__ __attribute__((aligned(16))) char stg0[STAGE_BYTES];
-    __shared__ __attribute__((aligned(16))) char stg1[STAGE_BYTES];
-    __shared__ __attribute__((aligned(16))) char stg2[STAGE_BYTES];
+    __shared__ __attribute__((aligned(16))) char stg[NSTG * Base::STAGE];
     const int64_t k0 = (int64_t)blockIdx.y * kchunk;
-    if (blockDim.x != NT || k0 >= K || kchunk % BK) return;
+    if (blockDim.x != NT || k0 >= K || kchunk % Base::TK) return;
     const int64_t kc = K - k0 < kchunk ? K - k0 : kchunk;
-    gemm_s_body<false>(A + k0, lda, B + k0 * ldb, ldb, W + (int64_t)blockIdx.y * M * N, N, M, N,
-                       kc, 1.0f, 0.0f, stg0, stg1, stg2, blockIdx.x, gridDim.x);
+    gemm_s_body<Base, false>(A + k0, lda, B + k0 * ldb, ldb, W + (int64_t)blockIdx.y * M * N, N,
+                             M, N, kc, 1.0f, 0.0f, stg, blockIdx.x, gridDim.x);
 }
 
 extern "C" __global__ __launch_bounds__(256) void gemm_splitk_reduce(const float *W, int32_t S,
@@ -361,9 +453,9 @@ extern "C" __global__ __launch_bounds__(NT, 1) void matmul(PHX_MEMREF2(float, a,
                                                             PHX_MEMREF2(float, b, int32_t),
                                                             PHX_MEMREF2(float, c, int32_t),
                                                             float alpha, float beta) {
-    GEMM_S_PRELUDE
-    gemm_s_body<true>(a_ptr + a_off, a_st0, b_ptr + b_off, b_st0, c_ptr + c_off, c_st0, M, N, K,
-                      alpha, beta, stg0, stg1, stg2, phx_block_linear(), phx_block_count());
+    GEMM_S_PRELUDE(Base)
+    gemm_s_body<Base, true>(a_ptr + a_off, a_st0, b_ptr + b_off, b_st0, c_ptr + c_off, c_st0, M,
+                            N, K, alpha, beta, stg, phx_block_linear(), phx_block_count());
 }
 
 // C = fl(beta * C) over a [M, N] tile: an HBM stream of 8 bytes per element.

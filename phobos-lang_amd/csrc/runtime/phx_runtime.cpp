@@ -459,6 +459,32 @@ static bool gemm_w8(phx_kernel k, int64_t M, int64_t N, int64_t K) {
     return M % PHX_H_BM == 0 && N % PHX_H_BN == 0 && K % PHX_H_BK == 0;
 }
 
+// The tilings of gemm_fp32 (entries of gemm_fp32.hsaco), by phx_plan
+// variant: the reference's autotuner picks TILE_M, TILE_N in [32, 256] and
+// TILE_K in [4, 32] (examples/gemm_fp32.ph:1); variant 0 is the built-in
+// 256 x 256 x 16 "gemm", the only one that also splits over K.
+struct S32Tiling {
+    const char *entry;
+    int64_t tm, tn, tk;
+};
+static const S32Tiling kS32[] = {
+    {"gemm", 256, 256, 16},           {"gemm_t256x128k16", 256, 128, 16},
+    {"gemm_t128x256k16", 128, 256, 16}, {"gemm_t128x128k16", 128, 128, 16},
+    {"gemm_t128x128k32", 128, 128, 32}, {"gemm_t128x128k8", 128, 128, 8},
+    {"gemm_t256x256k8", 256, 256, 8},   {"gemm_t64x64k16", 64, 64, 16},
+};
+constexpr int kS32Variants = (int)(sizeof kS32 / sizeof kS32[0]);
+
+// The gemm_fp32 tiling a launch at M x N x K uses: the pinned variant, else
+// the built-in one.
+static int s32_variant(int64_t M, int64_t N, int64_t K) {
+    phx_plan pin;
+    if (pinned_plan(gemm_key(PHX_GEMM_FP32, M, N, K), &pin) && pin.variant > 0 &&
+        pin.variant < kS32Variants)
+        return pin.variant;
+    return 0;
+}
+
 // K columns per chunk of a split into sp chunks (a multiple of 32).
 static int64_t split_chunk(int64_t K, int sp) {
     const int64_t steps = (K + PHX_SPLIT_KSTEP - 1) / PHX_SPLIT_KSTEP;
@@ -600,6 +626,19 @@ int launch_raw(hipFunction_t f, const uint32_t grid[3], const uint32_t block[3],
                 return launch_gemm_split_ws((phx_kernel)k, t, d[0], d[1], d[2], alpha, beta, sp,
                                             s, w.ptr);
             }
+            if (k == PHX_GEMM_FP32) {
+                if (const int v = s32_variant(d[0], d[1], d[2])) {
+                    const S32Tiling &ti = kS32[v];
+                    hipFunction_t fv;
+                    if (int rc = aux_function(kSpecs[k].file, ti.entry, &fv)) return rc;
+                    const uint32_t tiles = (uint32_t)(((d[0] + ti.tm - 1) / ti.tm) *
+                                                      ((d[1] + ti.tn - 1) / ti.tn));
+                    hipError_t e = hipModuleLaunchKernel(fv, tiles, 1, 1, PHX_S_THREADS, 1, 1, 0,
+                                                         s, args, nullptr);
+                    if (e != hipSuccess) return hip_error(e, "hipModuleLaunchKernel(gemm tiling)");
+                    return PHX_OK;
+                }
+            }
             if (gemm_w8((phx_kernel)k, d[0], d[1], d[2])) {
                 hipFunction_t fw;
                 if (int rc = aux_function(kSpecs[k].file, "gemm_w8", &fw)) return rc;
@@ -722,7 +761,11 @@ int grid_for(phx_kernel k, const int64_t *d, int nd, uint32_t grid[3], uint32_t 
     case PHX_GEMM_FP16:
         grid[0] = (uint32_t)(((d[0] + PHX_H_BM - 1) / PHX_H_BM) * ((d[1] + PHX_H_BN - 1) / PHX_H_BN));
         break;
-    case PHX_GEMM_FP32:
+    case PHX_GEMM_FP32: {
+        const S32Tiling &ti = kS32[s32_variant(d[0], d[1], d[2])];
+        grid[0] = (uint32_t)(((d[0] + ti.tm - 1) / ti.tm) * ((d[1] + ti.tn - 1) / ti.tn));
+        break;
+    }
     case PHX_MATMUL:
         grid[0] = (uint32_t)(((d[0] + PHX_S_TILE - 1) / PHX_S_TILE) *
                              ((d[1] + PHX_S_TILE - 1) / PHX_S_TILE));
@@ -1064,6 +1107,8 @@ int phx_plan_get(phx_kernel k, const int64_t *dims, int ndims, phx_plan *plan) {
         if (k == PHX_GEMM_FP16TC_FP32ACC && plan->splits == 1 &&
             !gemm_w8(k, dims[0], dims[1], dims[2]))
             plan->variant = 1;
+        if (k == PHX_GEMM_FP32 && plan->splits == 1)
+            plan->variant = s32_variant(dims[0], dims[1], dims[2]);
     } else if (is_flash(k)) {
         const bool bh = ndims == 4;
         plan->splits = flash_split(k, bh ? dims[0] : 1, dims[bh], dims[bh + 1]);
@@ -1085,9 +1130,15 @@ int phx_plan_pin(phx_kernel k, const int64_t *dims, int ndims, const phx_plan *p
     if (plan) {
         if (plan->splits < 1 || plan->splits > PHX_SPLIT_MAX)
             return set_error(PHX_E_INVALID, "splits %d outside 1..%d", plan->splits, PHX_SPLIT_MAX);
-        if (plan->variant != 0 && !(k == PHX_GEMM_FP16TC_FP32ACC && plan->variant == 1))
+        const bool tc1 = k == PHX_GEMM_FP16TC_FP32ACC && plan->variant == 1;
+        const bool s32 = k == PHX_GEMM_FP32 && plan->variant > 0 && plan->variant < kS32Variants;
+        if (plan->variant != 0 && !tc1 && !s32)
             return set_error(PHX_E_INVALID, "variant %d: kernel %d has no such variant",
                              plan->variant, (int)k);
+        if (s32 && plan->splits != 1)
+            return set_error(PHX_E_INVALID,
+                             "gemm_fp32 tiling %d (%s) runs unsplit; only variant 0 splits",
+                             plan->variant, kS32[plan->variant].entry);
     }
     std::lock_guard<std::mutex> lock(g_plan_mu);
     if (plan)

@@ -331,18 +331,51 @@ std::vector<Plan> split_space(int64_t units, bool variant1) {
     return out;
 }
 
-// Narrows the space to the pinned values (autotune.rs:38-58).
-std::vector<Plan> pin_space(std::vector<Plan> space, const std::map<std::string, int64_t> &pins) {
-    for (auto &kv : pins)
-        if (kv.first != "splits" && kv.first != "variant")
+// gemm_fp32's tilings by plan variant (TILE_M, TILE_N, TILE_K), as
+// include/phobos_hip.h lists them: the .ph file's @autotune dims.
+const int64_t kS32Tilings[][3] = {{256, 256, 16}, {256, 128, 16}, {128, 256, 16}, {128, 128, 16},
+                                  {128, 128, 32}, {128, 128, 8},  {256, 256, 8},  {64, 64, 16}};
+constexpr int kS32Count = (int)(sizeof kS32Tilings / sizeof kS32Tilings[0]);
+
+// Narrows the space to the pinned values (autotune.rs:38-58).  gemm_fp32
+// also takes TILE_M / TILE_N / TILE_K (dims not given keep the built-in
+// tiling's value), which select its tiling variant.
+std::vector<Plan> pin_space(std::vector<Plan> space, const std::map<std::string, int64_t> &pins,
+                            bool tiles = false) {
+    for (auto &kv : pins) {
+        const bool tile_dim = kv.first == "TILE_M" || kv.first == "TILE_N" || kv.first == "TILE_K";
+        if (kv.first != "splits" && kv.first != "variant" && !(tiles && tile_dim))
             throw Error(fmt("autotune pin '%s' is not a search dim of this kernel (dims: splits, "
-                            "variant)",
-                            kv.first.c_str()));
+                            "variant%s)",
+                            kv.first.c_str(), tiles ? ", TILE_M, TILE_N, TILE_K" : ""));
+    }
     if (pins.empty()) return space;
     Plan p{1, 0};
     if (pins.count("splits")) p.first = (int)pins.at("splits");
     if (pins.count("variant")) p.second = (int)pins.at("variant");
+    if (tiles && (pins.count("TILE_M") || pins.count("TILE_N") || pins.count("TILE_K"))) {
+        const char *names[3] = {"TILE_M", "TILE_N", "TILE_K"};
+        int64_t want[3];
+        for (int d = 0; d < 3; ++d) want[d] = pins.count(names[d]) ? pins.at(names[d]) : kS32Tilings[0][d];
+        p.second = -1;
+        for (int v = 0; v < kS32Count; ++v)
+            if (want[0] == kS32Tilings[v][0] && want[1] == kS32Tilings[v][1] &&
+                want[2] == kS32Tilings[v][2])
+                p.second = v;
+        if (p.second < 0)
+            throw Error(fmt("no gemm_fp32 tiling TILE_M=%lld TILE_N=%lld TILE_K=%lld",
+                            (long long)want[0], (long long)want[1], (long long)want[2]));
+    }
     return {p};
+}
+
+// A plan as the log names it: gemm_fp32 with its tile dims.
+std::string plan_str(phx_kernel k, const Plan &p) {
+    if (k == PHX_GEMM_FP32 && p.second >= 0 && p.second < kS32Count)
+        return fmt("splits=%d variant=%d (TILE_M=%lld TILE_N=%lld TILE_K=%lld)", p.first, p.second,
+                   (long long)kS32Tilings[p.second][0], (long long)kS32Tilings[p.second][1],
+                   (long long)kS32Tilings[p.second][2]);
+    return plan_str(p);
 }
 
 struct Tuner {
@@ -374,10 +407,10 @@ struct Tuner {
                 for (int w = 0; w < WARMUP; ++w) launch();
                 double best = 1e30;
                 for (int i = 0; i < PROBES_SHORT; ++i) best = std::min(best, probe());
-                info(fmt("  %s: %.2f us", plan_str(p).c_str(), best * 1e6));
+                info(fmt("  %s: %.2f us", plan_str(kernel, p).c_str(), best * 1e6));
                 cand.push_back({best, p});
             } catch (const Error &e) {
-                info(fmt("  %s: skipped (%s)", plan_str(p).c_str(), e.what()));
+                info(fmt("  %s: skipped (%s)", plan_str(kernel, p).c_str(), e.what()));
             }
         }
         if (cand.empty()) throw Error("autotune: no config works");
@@ -398,12 +431,12 @@ struct Tuner {
             }
         size_t best = 0;
         for (size_t i = 0; i < cand.size(); ++i) {
-            info(fmt("  %s: %.2f us (spread %.2f us)", plan_str(cand[i].second).c_str(),
+            info(fmt("  %s: %.2f us (spread %.2f us)", plan_str(kernel, cand[i].second).c_str(),
                      mn[i] * 1e6, (mx[i] - mn[i]) * 1e6));
             if (mn[i] < mn[best]) best = i;
         }
         pin(cand[best].second);
-        info("autotune winner: " + plan_str(cand[best].second));
+        info("autotune winner: " + plan_str(kernel, cand[best].second));
         return cand[best].second;
     }
 };
@@ -623,7 +656,10 @@ void bench_gemm(Ctx &cx, const char *name, const char *ph, phx_kernel kern, bool
                     verify_matmul(c, a, b, alpha, beta, M, N, K, f16_inputs);
                 }
             }};
-    t.run(pin_space(split_space(K / 32, kern == PHX_GEMM_FP16TC_FP32ACC), cx.opt.pins));
+    std::vector<Plan> space = split_space(K / 32, kern == PHX_GEMM_FP16TC_FP32ACC);
+    if (kern == PHX_GEMM_FP32)  // the other tilings, unsplit
+        for (int v = 1; v < kS32Count; ++v) space.push_back({1, v});
+    t.run(pin_space(space, cx.opt.pins, kern == PHX_GEMM_FP32));
     const double s = bench(fmt("phobos %s", name).c_str(), t.launch);
     t.verify();
     info(fmt("check: %lld elements sampled at 64 points, correct", (long long)(M * N)));

@@ -358,6 +358,11 @@ def _addr(buf, nbytes, what):
     return int(buf)
 
 
+# gemm_fp32's tilings by launch-plan variant (TILE_M, TILE_N, TILE_K), as
+# include/phobos_hip.h lists them; variant 0 is the built-in tiling.
+GEMM_FP32_TILINGS = [(256, 256, 16), (256, 128, 16), (128, 256, 16), (128, 128, 16),
+                     (128, 128, 32), (128, 128, 8), (256, 256, 8), (64, 64, 16)]
+
 _GEMM_ESZ = {GEMM_FP32: 4, GEMM_FP16TC_FP32ACC: 4, GEMM_FP16: 2, MATMUL: 4}
 
 

@@ -10,10 +10,11 @@ launches for about 200 us (one launch when that is longer), timed with HIP
 events on the launch stream; in the round-robin each probe follows one
 untimed launch of the same plan, so it does not inherit the previous plan's
 cache contents (a split plan's partial sums can push the operands out of
-the 256 MB MALL, which the next plan would then pay for).  The MI355X kernels have one tile shape each, so the space
-here is the launch plan (phx_plan): the number of K chunks of a GEMM or key
-chunks of a flash launch, and for gemm_fp16tc_fp32acc on whole tiles which
-of its two kernels runs.  The winner is pinned with phx_plan_pin, so every
+the 256 MB MALL, which the next plan would then pay for).  The space here
+is the launch plan (phx_plan): the number of K chunks of a GEMM or key
+chunks of a flash launch, gemm_fp32's tile dims (TILE_M x TILE_N x TILE_K
+over the reference's ranges), and for gemm_fp16tc_fp32acc on whole tiles
+which of its two kernels runs.  The winner is pinned with phx_plan_pin, so every
 later launch of that kernel at that shape uses it.
 
 A candidate is verified on its first launch against the unsplit plan's
@@ -26,6 +27,7 @@ import math
 import numpy as np
 
 from . import (FLASH_FP16, FLASH_FP16_BH, FLASH_FP32_BH, GEMM_FP16, GEMM_FP16TC_FP32ACC,
+               GEMM_FP32, GEMM_FP32_TILINGS,
                DeviceBuffer, Event, PhxError, bind_workspace, get_workspace, launch_flash,
                launch_flash_bh, launch_gemm, normal_f32, plan_pin, to_f16_bits)
 
@@ -45,17 +47,54 @@ def _effective(units, sp):
 
 
 def gemm_space(kernel, M, N, K):
-    """[(splits, variant)] for a GEMM: every distinct split count, and for
-    gemm_fp16tc_fp32acc on whole 256 x 256 tiles the one-wave kernel too."""
+    """[(splits, variant)] for a GEMM: every distinct split count; for
+    gemm_fp32 every other tiling (TILE_M x TILE_N x TILE_K, the @autotune
+    dims of examples/gemm_fp32.ph:1), unsplit; for gemm_fp16tc_fp32acc on
+    whole 256 x 256 tiles the one-wave kernel too."""
     steps = -(-K // 32)
     space = []
     for sp in SPLITS:
         e = _effective(steps, sp)
         if (e, 0) not in space and (e == 1 or e * M * N * 4 <= MAX_WORKSPACE):
             space.append((e, 0))
+    if kernel == GEMM_FP32:
+        space += [(1, v) for v in range(1, len(GEMM_FP32_TILINGS))]
     if kernel == GEMM_FP16TC_FP32ACC and M % 256 == 0 and N % 256 == 0 and K % 32 == 0:
         space.append((1, 1))
     return space
+
+
+def search_dims(kernel):
+    """Names a --autotune pin may set for kernel (autotune.rs:38-58 checks
+    pins against the kernel's @autotune dims)."""
+    if kernel == GEMM_FP32:
+        return ("splits", "variant", "TILE_M", "TILE_N", "TILE_K")
+    return ("splits", "variant")
+
+
+def plan_from_pins(kernel, pins):
+    """The (splits, variant) plan that NAME=VALUE pins name.  For gemm_fp32
+    TILE_M / TILE_N / TILE_K select the tiling (dims not given keep the
+    built-in 256 x 256 x 16's value); PhxError if no tiling has them."""
+    sp, v = pins.get("splits", 1), pins.get("variant", 0)
+    tile = [pins.get(d) for d in ("TILE_M", "TILE_N", "TILE_K")]
+    if kernel == GEMM_FP32 and any(t is not None for t in tile):
+        want = tuple(t if t is not None else b for t, b in zip(tile, GEMM_FP32_TILINGS[0]))
+        if want not in GEMM_FP32_TILINGS:
+            raise PhxError(-1, f"no gemm_fp32 tiling TILE_M={want[0]} TILE_N={want[1]} "
+                               f"TILE_K={want[2]}; tilings: " +
+                               ", ".join("%dx%dx%d" % t for t in GEMM_FP32_TILINGS))
+        v = GEMM_FP32_TILINGS.index(want)
+    return sp, v
+
+
+def plan_name(kernel, plan):
+    """A readable name of a (splits, variant) plan: gemm_fp32's tiling dims."""
+    sp, v = plan
+    if kernel == GEMM_FP32:
+        tm, tn, tk = GEMM_FP32_TILINGS[v]
+        return f"TILE_M={tm} TILE_N={tn} TILE_K={tk} splits={sp}"
+    return f"splits={sp} variant={v}"
 
 
 def flash_space(BH, Nq, Nk):

@@ -91,7 +91,8 @@ def test_pins_take_effect_and_come_off(px_gpu, stream):
 def test_invalid_pins_are_refused(px_gpu):
     px = px_gpu
     dims = [512, 512, 512]
-    for sp, var, kern in ((0, 0, px.GEMM_FP32), (17, 0, px.GEMM_FP32), (1, 1, px.GEMM_FP32),
+    for sp, var, kern in ((0, 0, px.GEMM_FP32), (17, 0, px.GEMM_FP32), (1, 8, px.GEMM_FP32),
+                          (2, 1, px.GEMM_FP32),
                           (1, 2, px.GEMM_FP16TC_FP32ACC), (1, 1, px.GEMM_FP16)):
         with pytest.raises(px.PhxError):
             px.plan_pin(kern, dims, sp, var)

@@ -88,9 +88,21 @@ def test_pins_override_the_rule_and_come_off():
 
 def test_pin_validation():
     dims = [512, 512, 4096]
-    for sp, var in ((0, 0), (17, 0), (1, 1), (1, -1)):
+    for sp, var in ((0, 0), (17, 0), (1, 8), (1, -1), (2, 1)):
         with pytest.raises(px.PhxError):
             px.plan_pin(px.GEMM_FP32, dims, sp, var)
+    for sp, var in ((1, 1), (1, 7)):  # gemm_fp16 has no tilings to choose from
+        with pytest.raises(px.PhxError):
+            px.plan_pin(px.GEMM_FP16, dims, sp, var)
+    # gemm_fp32's tilings: pinned unsplit, and the grid follows the tile
+    px.plan_pin(px.GEMM_FP32, dims, 1, 3)  # 128 x 128 x 16
+    assert px.plan_get(px.GEMM_FP32, dims) == (1, 3)
+    assert px.split_plan(px.GEMM_FP32, dims) == (1, 0)
+    assert px.grid_for(px.GEMM_FP32, dims)[0] == (16, 1, 1)
+    px.plan_pin(px.GEMM_FP32, dims, 1, 7)  # 64 x 64 x 16
+    assert px.grid_for(px.GEMM_FP32, dims)[0] == (64, 1, 1)
+    px.plan_pin(px.GEMM_FP32, dims, None)
+    assert px.grid_for(px.GEMM_FP32, dims)[0] == (4, 1, 1)
     px.plan_pin(px.GEMM_FP16TC_FP32ACC, dims, 1, 1)
     assert px.plan_get(px.GEMM_FP16TC_FP32ACC, dims) == (1, 1)
     # a pinned count is rounded like a requested one (whole steps, no empty chunk)
