@@ -286,6 +286,32 @@ def shapes_leg(px, stream, reps=20, tune=True):
     return out
 
 
+def hbm_ceiling_leg(px, sets=4, nbytes=256 << 20, reps=3):
+    """The box's practical HBM ceiling next to saxpy's figure: hipMemcpy
+    device-to-device (phx_memcpy_d2d) of 256 MiB, rotating over `sets`
+    source/destination pairs (1 GiB each way, past the 256 MB MALL), timed
+    with HIP events on the legacy stream; bytes read + written per second."""
+    bufs = [(px.DeviceBuffer(nbytes), px.DeviceBuffer(nbytes)) for _ in range(sets)]
+    for src, dst in bufs:  # first touch
+        px.check(px.lib().phx_memcpy_d2d(dst.ptr, src.ptr, nbytes))
+    px.synchronize()
+    e0, e1 = px.Event(), px.Event()
+    best = None
+    for _ in range(reps):
+        e0.record(None)
+        for src, dst in bufs:
+            px.check(px.lib().phx_memcpy_d2d(dst.ptr, src.ptr, nbytes))
+        e1.record(None)
+        e1.synchronize()
+        ms = e0.elapsed_ms(e1)
+        best = ms if best is None else min(best, ms)
+    for src, dst in bufs:
+        src.free()
+        dst.free()
+    return {"what": "hipMemcpy device-to-device, 256 MiB x %d sets" % sets,
+            "value": round(2 * nbytes * sets / (best / 1e3) / 1e9, 1), "unit": "GB/s"}
+
+
 def autotune_leg(px, stream, wanted, pins):
     """The launch-plan search of every benchmark kernel at its BASELINE
     shape and arguments, before the timed steps, as phobos-bench tunes each
@@ -620,6 +646,14 @@ def main():
         log(f"{k.name:22s} avg {avg:8.4f} ms  min {t.min():8.4f} ms  "
             f"{val:10.2f} {k.unit}  ({100 * val / k.peak:5.1f}% of peak)")
 
+    if "saxpy_fp32" in kern:
+        try:
+            ceil = hbm_ceiling_leg(px)
+            ceil["saxpy_frac_of_it"] = round(kern["saxpy_fp32"]["value"] / ceil["value"], 3)
+        except px.PhxError as e:
+            ceil = {"error": str(e)}
+        kern["saxpy_fp32"]["hbm_copy_ceiling"] = ceil
+        log(f"hbm ceiling on this box: {ceil}")
     if args.csv:
         write_results_csv(args, kern, wanted)
     head = "gemm_fp16tc_fp32acc"
