@@ -47,6 +47,22 @@
 // MFMA GEMMs, whose K steps are 8x cheaper) 32-deep steps: measured on
 // MI355X at 512^3 .. 2048^3 and 256^2 x 16384, shorter f16 chunks lose more
 // to the partial-sum traffic than they gain.
+// gemm_fp32's built-in tiling (no pin): 256 x 256 x 16 when its tiles fill
+// all PHX_S32_FULL_TILES CUs; else 64 x 64 x 16 (launch-plan variant
+// PHX_S32_SMALL_VARIANT) when that gives at least PHX_S32_SMALL_MIN_TILES
+// tiles, or at least PHX_S32_SMALL_SHORT_TILES with K <= PHX_S32_SHORT_K;
+// else the split rule below.  Measured on MI355X (one box, HIP events): the
+// small tile beats both the 256 x 256 tile and its split at 3072^2 x 1024
+// (151 vs 260 us unsplit), 2048^3 (133 vs 160 split), 768^3 (18.5 vs 44),
+// 1024^2 x 256 (9 vs 40) and 512^2 x 2048 (41 vs 58); the split stays ahead
+// only with long K over few tiles (512^2 x 16384: 255 vs 300 us).
+#define PHX_S32_FULL_TILES 256
+#define PHX_S32_SMALL_VARIANT 7
+#define PHX_S32_SMALL_TILE 64
+#define PHX_S32_SMALL_MIN_TILES 128
+#define PHX_S32_SMALL_SHORT_TILES 16
+#define PHX_S32_SHORT_K 4096
+
 #define PHX_SPLIT_MIN_TILES 128
 #define PHX_SPLIT_MAX 16
 #define PHX_SPLIT_MIN_STEPS_F32 1

@@ -416,6 +416,47 @@ int fit_split(int64_t units, int sp, size_t bytes_per_chunk, size_t cap) {
 }
 }  // namespace
 
+// The tilings of gemm_fp32 (entries of gemm_fp32.hsaco), by phx_plan
+// variant: the reference's autotuner picks TILE_M, TILE_N in [32, 256] and
+// TILE_K in [4, 32] (examples/gemm_fp32.ph:1); variant 0 is the built-in
+// 256 x 256 x 16 "gemm", the only one that also splits over K.
+struct S32Tiling {
+    const char *entry;
+    int64_t tm, tn, tk;
+};
+static const S32Tiling kS32[] = {
+    {"gemm", 256, 256, 16},           {"gemm_t256x128k16", 256, 128, 16},
+    {"gemm_t128x256k16", 128, 256, 16}, {"gemm_t128x128k16", 128, 128, 16},
+    {"gemm_t128x128k32", 128, 128, 32}, {"gemm_t128x128k8", 128, 128, 8},
+    {"gemm_t256x256k8", 256, 256, 8},   {"gemm_t64x64k16", 64, 64, 16},
+};
+constexpr int kS32Variants = (int)(sizeof kS32 / sizeof kS32[0]);
+
+// The built-in gemm_fp32 tiling (no pin): the 256 x 256 tile when it fills
+// the GPU, else the 64 x 64 one where it measured faster than splitting K
+// (phx_geometry.h), else 0 and the split rule.
+static int s32_rule(int64_t M, int64_t N, int64_t K) {
+    const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
+    if (t256 >= PHX_S32_FULL_TILES) return 0;
+    const int64_t ts = PHX_S32_SMALL_TILE;
+    const int64_t tsmall = ((M + ts - 1) / ts) * ((N + ts - 1) / ts);
+    if (tsmall >= PHX_S32_SMALL_MIN_TILES ||
+        (tsmall >= PHX_S32_SMALL_SHORT_TILES && K <= PHX_S32_SHORT_K))
+        return PHX_S32_SMALL_VARIANT;
+    return 0;
+}
+
+// The gemm_fp32 tiling a launch at M x N x K uses: the pinned variant, else
+// (unless PHX_GEMM_SPLIT forces a split of the 256 x 256 tiling) the
+// built-in one.
+static int s32_variant(int64_t M, int64_t N, int64_t K) {
+    phx_plan pin;
+    if (pinned_plan(gemm_key(PHX_GEMM_FP32, M, N, K), &pin))
+        return pin.variant > 0 && pin.variant < kS32Variants ? pin.variant : 0;
+    if (getenv("PHX_GEMM_SPLIT")) return 0;
+    return s32_rule(M, N, K);
+}
+
 // How many K chunks a GEMM is split into (1: no split).  A GEMM whose
 // 256 x 256 output tiles cannot fill half of the 256 CUs gets enough chunks
 // to give every CU a workgroup, within the chunk-length floor of its kernel
@@ -431,6 +472,7 @@ int gemm_split(phx_kernel k, int64_t M, int64_t N, int64_t K) {
     } else if (pinned_plan(gemm_key(k, M, N, K), &pin)) {
         sp = pin.splits;
     } else {
+        if (k == PHX_GEMM_FP32 && s32_rule(M, N, K) != 0) return 1;  // a smaller tile instead
         if (tiles >= PHX_SPLIT_MIN_TILES) return 1;
         const int64_t min_steps =
             k == PHX_GEMM_FP32 ? PHX_SPLIT_MIN_STEPS_F32 : PHX_SPLIT_MIN_STEPS_F16;
@@ -457,32 +499,6 @@ static bool gemm_w8(phx_kernel k, int64_t M, int64_t N, int64_t K) {
         return false;
     }
     return M % PHX_H_BM == 0 && N % PHX_H_BN == 0 && K % PHX_H_BK == 0;
-}
-
-// The tilings of gemm_fp32 (entries of gemm_fp32.hsaco), by phx_plan
-// variant: the reference's autotuner picks TILE_M, TILE_N in [32, 256] and
-// TILE_K in [4, 32] (examples/gemm_fp32.ph:1); variant 0 is the built-in
-// 256 x 256 x 16 "gemm", the only one that also splits over K.
-struct S32Tiling {
-    const char *entry;
-    int64_t tm, tn, tk;
-};
-static const S32Tiling kS32[] = {
-    {"gemm", 256, 256, 16},           {"gemm_t256x128k16", 256, 128, 16},
-    {"gemm_t128x256k16", 128, 256, 16}, {"gemm_t128x128k16", 128, 128, 16},
-    {"gemm_t128x128k32", 128, 128, 32}, {"gemm_t128x128k8", 128, 128, 8},
-    {"gemm_t256x256k8", 256, 256, 8},   {"gemm_t64x64k16", 64, 64, 16},
-};
-constexpr int kS32Variants = (int)(sizeof kS32 / sizeof kS32[0]);
-
-// The gemm_fp32 tiling a launch at M x N x K uses: the pinned variant, else
-// the built-in one.
-static int s32_variant(int64_t M, int64_t N, int64_t K) {
-    phx_plan pin;
-    if (pinned_plan(gemm_key(PHX_GEMM_FP32, M, N, K), &pin) && pin.variant > 0 &&
-        pin.variant < kS32Variants)
-        return pin.variant;
-    return 0;
 }
 
 // K columns per chunk of a split into sp chunks (a multiple of 32).

@@ -65,7 +65,9 @@ def test_grid_for_and_shape_checks():
     assert g == (256, 1, 1) and b == (256, 1, 1)
     g, b = px.grid_for(px.GEMM_FP32, [4096, 4096, 4096])
     assert g == (256, 1, 1)
-    g, b = px.grid_for(px.GEMM_FP32, [384, 640, 32])  # 256-wide tiles, the last ones partial
+    g, b = px.grid_for(px.GEMM_FP32, [384, 640, 32])  # the 64 x 64 tiling at this size
+    assert g == (6 * 10, 1, 1)
+    g, b = px.grid_for(px.GEMM_FP16, [384, 640, 32])  # 256-wide tiles, the last ones partial
     assert g == (6, 1, 1)
     g, b = px.grid_for(px.FLASH_FP16_BH, [64, 4096, 4096, 64])
     assert g == (16, 64, 1) and b == (512, 1, 1)  # f16: 8 waves x 32 queries

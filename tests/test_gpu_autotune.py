@@ -60,7 +60,8 @@ def test_plan_get_reports_the_built_in_rule(px_gpu):
     for kern in (px.GEMM_FP32, px.GEMM_FP16TC_FP32ACC, px.GEMM_FP16):
         assert px.plan_get(kern, [4096, 4096, 4096]) == (1, 0)
         assert px.plan_get(kern, [512, 512, 4096])[0] == px.split_plan(kern, [512, 512, 4096])[0]
-    assert px.plan_get(px.GEMM_FP32, [1024, 1024, 1024])[0] == 16
+    assert px.plan_get(px.GEMM_FP32, [1024, 1024, 1024]) == (1, 7)  # the 64 x 64 tiling
+    assert px.plan_get(px.GEMM_FP32, [256, 256, 8192]) == (16, 0)  # long K, few tiles: split
     assert px.plan_get(px.FLASH_FP16_BH, [64, 4096, 4096, 64]) == (1, 0)
     assert px.plan_get(px.FLASH_FP16, [4096, 4096, 64])[0] > 1
 
@@ -68,7 +69,7 @@ def test_plan_get_reports_the_built_in_rule(px_gpu):
 def test_pins_take_effect_and_come_off(px_gpu, stream):
     px = px_gpu
     kern, dims = px.GEMM_FP32, [1024, 1024, 1024]
-    run, want = _gemm_case(px, stream, kern, *dims)
+    run, want = _gemm_case(px, stream, kern, *dims)  # built-in: 64 x 64 x 16, unsplit
     auto = px.plan_get(kern, dims)
     for sp in (1, 3, 16):
         px.plan_pin(kern, dims, sp)
@@ -82,7 +83,7 @@ def test_pins_take_effect_and_come_off(px_gpu, stream):
     other_kernel = px.plan_get(px.GEMM_FP16, dims)
     px.plan_pin(kern, dims, 2)
     assert px.plan_get(kern, dims) == (2, 0)
-    assert px.plan_get(kern, [1024, 1024, 2048]) == other_shape == (16, 0)
+    assert px.plan_get(kern, [1024, 1024, 2048]) == other_shape == (1, 7)
     assert px.plan_get(px.GEMM_FP16, dims) == other_kernel
     px.plan_unpin_all()
     assert px.plan_get(kern, dims) == auto

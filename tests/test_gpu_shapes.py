@@ -88,7 +88,11 @@ def test_small_gemms_against_oracle(px_gpu, stream, kern_name, M, N, K):
     px = px_gpu
     kern = getattr(px, kern_name)
     sp, ws = px.split_plan(kern, [M, N, K])
-    if kern_name == "GEMM_FP32" or K >= 4096:
+    if kern_name == "GEMM_FP32":
+        # the 64 x 64 tiling where it fills the GPU at this K, else the split
+        small = px.plan_get(kern, [M, N, K])[1] == 7
+        assert (sp == 1) == small and ws == (0 if small else sp * M * N * 4), (sp, ws)
+    elif K >= 4096:
         assert sp > 1 and ws == sp * M * N * 4, (sp, ws)
     A = oracle.normal_f32(21, M * K, 1 / np.sqrt(K)).reshape(M, K)
     B = oracle.normal_f32(22, K * N, 1 / np.sqrt(K)).reshape(K, N)

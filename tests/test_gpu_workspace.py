@@ -8,8 +8,8 @@ results go to the workspace bound to the launch stream
 (phx_stream_set_workspace), or, in a pod, to an arena slab.  Checked here:
 
   * the reference bench's own one-head 4096 x 4096 flash launch
-    (phx_launch_by_name with the .ph geometry, main.rs:334-371) and a 512^3
-    gemm_fp32 through phx_compute run split inside the bound workspace (its
+    (phx_launch_by_name with the .ph geometry, main.rs:334-371) and a
+    256 x 256 x 8192 gemm_fp32 through phx_compute run split inside the bound workspace (its
     sentinel bytes are overwritten), leave hipMemGetInfo's free bytes
     unchanged, and meet the oracle;
   * the same launches on a stream with no workspace run unsplit, allocate
@@ -90,7 +90,7 @@ def _one_head_flash(px, stream, Nq=4096, Nk=4096, D=64, scale=0.125, seed=5):
     return launch, check, (dq, dk, dv, do, keep)
 
 
-def _gemm_fp32_compute(px, stream, M=512, N=512, K=512, alpha=0.125, beta=1.5, seed=11):
+def _gemm_fp32_compute(px, stream, M=256, N=256, K=8192, alpha=0.125, beta=1.5, seed=11):
     a, b, c = (oracle.lcg_f32(seed + i, n) for i, n in enumerate((M * K, K * N, M * N)))
     da, db, dc = (px.DeviceBuffer.from_array(t) for t in (a, b, c))
     fn = px.builtin_function(px.GEMM_FP32)
@@ -100,7 +100,7 @@ def _gemm_fp32_compute(px, stream, M=512, N=512, K=512, alpha=0.125, beta=1.5, s
         dc.upload(c)
         px.compute(fn, 32, [(da.ptr, (M, K)), (db.ptr, (K, N)), (dc.ptr, (M, N))],
                    [(3, 4, px.f32_bits(alpha)), (4, 4, px.f32_bits(beta))],
-                   (M // 128, N // 128, 1), (256, 1, 1), stream)
+                   (M // 128, N // 128, 1), (256, 1, 1), stream)  # the reference's geometry
 
     def check():
         got = dc.download(np.float32, M * N).reshape(M, N)
@@ -164,14 +164,14 @@ def test_unbound_stream_runs_unsplit_and_allocates_nothing(px_gpu, bare_stream):
 
 def test_gemm_compute_splits_inside_the_bound_workspace(px_gpu, bare_stream):
     px, s = px_gpu, bare_stream
-    sp, need = px.split_plan(px.GEMM_FP32, [512, 512, 512])
-    assert sp > 1 and need == sp * 512 * 512 * 4
+    sp, need = px.split_plan(px.GEMM_FP32, [256, 256, 8192])
+    assert sp == 16 and need == sp * 256 * 256 * 4
     ws = px.DeviceBuffer(need)
     px.set_workspace(s, ws.ptr, need)
     launch, check, _ = _gemm_fp32_compute(px, s)
     assert _run_checked(px, s, launch, check, ws)
     # a workspace that holds three chunks: the launch takes at most three
-    small = 3 * 512 * 512 * 4
+    small = 3 * 256 * 256 * 4
     px.set_workspace(s, ws.ptr, small)
     px.check(px.lib().phx_memset_async(ws.ptr, SENTINEL, need, None))
     px.synchronize()
@@ -180,6 +180,10 @@ def test_gemm_compute_splits_inside_the_bound_workspace(px_gpu, bare_stream):
     check()
     w = ws.download(np.uint8, need)
     assert (w[:small] != SENTINEL).any() and (w[small:] == SENTINEL).all()
+    # 512^3 runs the 64 x 64 tiling unsplit: nothing allocated either
+    assert px.split_plan(px.GEMM_FP32, [512, 512, 512]) == (1, 0)
+    launch2, check2, _ = _gemm_fp32_compute(px, s, 512, 512, 512, seed=61)
+    _run_checked(px, s, launch2, check2)
     px.set_workspace(s, 0, 0)
 
 
@@ -190,14 +194,14 @@ def test_misaligned_workspace_is_refused(px_gpu, bare_stream):
 
 
 def test_pod_split_compute_takes_an_arena_slab(px_gpu, tmp_path):
-    # A 512^3 gemm_fp32 COMPUTE (split 16 ways by the built-in rule) in a
-    # pod: the tiles take 3 MiB of the arena and the split's partial sums
-    # another 16 MiB slab while the leaf runs; free device memory is the
+    # A 256 x 256 x 8192 gemm_fp32 COMPUTE (split 16 ways by the built-in
+    # rule) in a pod: the tiles take 16.25 MiB of the arena and the split's
+    # partial sums another 4 MiB slab while the leaf runs; free device memory is the
     # same before and after the segment.  With an arena too small for the
     # slab the leaf runs unsplit, to the same bound.
     from phobos_amd import cluster as cl
     px = px_gpu
-    M = N = K = 512
+    M, N, K = 256, 256, 8192
     alpha, beta = 0.125, 1.5
     sp, need = px.split_plan(px.GEMM_FP32, [M, N, K])
     assert sp > 1

@@ -4,7 +4,9 @@ split rule is restated here independently (phx_geometry.h's constants:
 256 x 256 output tiles, 32-deep K steps, at least 128 tiles or 256 of 512
 flash slots before anything splits, at most 16 chunks, at least 1 K step per
 chunk for gemm_fp32 and 32 for the f16 GEMMs, at least 8 key blocks per flash
-chunk, no empty chunk) and compared over a grid of shapes."""
+chunk, no empty chunk; gemm_fp32 takes its 64 x 64 x 16 tiling instead of a
+split below 256 tiles of 256 x 256 when that gives at least 128 tiles, or 16
+with K <= 4096) and compared over a grid of shapes."""
 import itertools
 
 import pytest
@@ -27,9 +29,19 @@ def _rounded(units, sp):
     return -(-units // per)
 
 
+def _s32_tiling(M, N, K):
+    """gemm_fp32's built-in tiling variant: 0 (256 x 256 x 16) or 7 (64 x 64 x 16)."""
+    if -(-M // 256) * -(-N // 256) >= 256:
+        return 0
+    small = -(-M // 64) * -(-N // 64)
+    return 7 if small >= 128 or (small >= 16 and K <= 4096) else 0
+
+
 def _gemm_rule(kern, M, N, K):
     tiles = -(-M // 256) * -(-N // 256)
     steps = -(-K // 32)
+    if kern == px.GEMM_FP32 and _s32_tiling(M, N, K):
+        return 1
     if tiles >= 128:
         return 1
     sp = min(256 // tiles, steps // (1 if kern == px.GEMM_FP32 else 32), 16)
@@ -59,6 +71,19 @@ def test_gemm_split_rule(name):
         assert sp == want, (M, N, K, sp, want)
         assert ws == (sp * M * N * 4 if sp > 1 else 0)
         assert px.plan_get(kern, [M, N, K])[0] == want
+        if kern == px.GEMM_FP32:
+            v = _s32_tiling(M, N, K)
+            assert px.plan_get(kern, [M, N, K]) == (want, v)
+            tm, tn, _ = px.GEMM_FP32_TILINGS[v]
+            assert px.grid_for(kern, [M, N, K])[0] == (-(-M // tm) * -(-N // tn), 1, 1)
+
+
+def test_gemm_fp32_small_tiling_is_64x64():
+    assert px.GEMM_FP32_TILINGS[7] == (64, 64, 16)
+    assert px.plan_get(px.GEMM_FP32, [3072, 3072, 1024]) == (1, 7)
+    assert px.plan_get(px.GEMM_FP32, [4096, 4096, 4096]) == (1, 0)
+    assert px.plan_get(px.GEMM_FP32, [512, 512, 16384])[1] == 0  # long K, few tiles: split
+    assert px.plan_get(px.GEMM_FP32, [512, 512, 16384])[0] > 1
 
 
 @pytest.mark.parametrize("f16", [True, False])
@@ -74,11 +99,12 @@ def test_flash_split_rule(f16):
 
 
 def test_pins_override_the_rule_and_come_off():
-    dims = [512, 512, 4096]
+    dims = [512, 512, 8192]
     rule = px.plan_get(px.GEMM_FP32, dims)
     px.plan_pin(px.GEMM_FP32, dims, 3)
     assert px.plan_get(px.GEMM_FP32, dims) == (3, 0)
     assert px.split_plan(px.GEMM_FP32, dims) == (3, 3 * 512 * 512 * 4)
+    assert px.plan_get(px.GEMM_FP32, [512, 512, 4096]) == (1, 7)  # pins are per shape
     with pytest.raises(px.PhxError, match="outside 1..16"):
         px.plan_pin(px.GEMM_FP32, dims, 500)
     assert px.plan_get(px.GEMM_FP32, dims) == (3, 0)  # a refused pin leaves the old one
@@ -101,8 +127,10 @@ def test_pin_validation():
     assert px.grid_for(px.GEMM_FP32, dims)[0] == (16, 1, 1)
     px.plan_pin(px.GEMM_FP32, dims, 1, 7)  # 64 x 64 x 16
     assert px.grid_for(px.GEMM_FP32, dims)[0] == (64, 1, 1)
-    px.plan_pin(px.GEMM_FP32, dims, None)
+    px.plan_pin(px.GEMM_FP32, dims, 1, 0)  # 256 x 256 x 16
     assert px.grid_for(px.GEMM_FP32, dims)[0] == (4, 1, 1)
+    px.plan_pin(px.GEMM_FP32, dims, None)  # the built-in plan here: 64 x 64 x 16
+    assert px.plan_get(px.GEMM_FP32, dims) == (1, 7)
     px.plan_pin(px.GEMM_FP16TC_FP32ACC, dims, 1, 1)
     assert px.plan_get(px.GEMM_FP16TC_FP32ACC, dims) == (1, 1)
     # a pinned count is rounded like a requested one (whole steps, no empty chunk)
