@@ -65,3 +65,14 @@ def test_unknown_pin_dim_is_refused():
     r = _run("--bench", "gemm_fp16", "--autotune", "TILE_M=256")
     assert r.returncode == 1
     assert "autotune pin 'TILE_M' is not a search dim of this kernel (dims: splits, variant)" in r.stderr
+
+
+@pytest.mark.gpu
+def test_gemm_fp32_tile_pin_by_reference_dim_names():
+    # gemm_fp32.ph's @autotune dims (examples/gemm_fp32.ph:1) as pins: the
+    # 128 x 128 x 32 tiling runs and passes the reference's 64-point check
+    r = _run("--bench", "gemm_fp32", "--autotune", "TILE_M=128 TILE_N=128 TILE_K=32")
+    assert r.returncode == 0, r.stderr
+    assert "TILE_M=128 TILE_N=128 TILE_K=32" in r.stdout and "correct" in r.stdout
+    r = _run("--bench", "gemm_fp32", "--autotune", "TILE_M=96")
+    assert r.returncode == 1 and "no gemm_fp32 tiling TILE_M=96" in r.stderr
