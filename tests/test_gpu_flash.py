@@ -125,6 +125,28 @@ def test_flash_baseline_config_sampled(px_gpu, stream, bits):
     assert worst < TOL[bits], worst
 
 
+@pytest.mark.parametrize("bits", [16, 32])
+def test_flash_baseline_config_every_row(px_gpu, stream, bits):
+    # all 64 heads x 4096 rows of the BASELINE config against the f64
+    # online-softmax replay (main.rs:894-911, OpenMP over rows), and the
+    # convexity bound: each output row is a convex combination of V's rows
+    BH, N, D = 64, 4096, 64
+    q, k, v = _inputs((BH, N, D), bits, 1)
+    dq, dk, dv = (_upload(px_gpu, t, bits) for t in (q, k, v))
+    do = px_gpu.DeviceBuffer(BH * N * D * 4)
+    kb = px_gpu.FLASH_FP16_BH if bits == 16 else px_gpu.FLASH_FP32_BH
+    px_gpu.launch_flash_bh(stream, kb, dq.ptr, dk.ptr, dv.ptr, do.ptr, BH, N, N, D, 0.125)
+    stream.synchronize()
+    got = _download(do, (BH, N, D), bits)
+    want = oracle.flash_heads(q, k, v, 0.125)
+    assert _rel(got, want) < TOL[bits]
+    vmax = np.abs(v).reshape(BH, -1).max(axis=1)
+    vmin_col, vmax_col = v.min(axis=1), v.max(axis=1)  # per head and d
+    slack = 1e-2 if bits == 16 else 1e-5
+    assert (np.abs(got).reshape(BH, -1).max(axis=1) <= vmax * (1 + slack)).all()
+    assert (got >= vmin_col[:, None, :] - slack).all() and (got <= vmax_col[:, None, :] + slack).all()
+
+
 def test_flash16_rows_past_nq_untouched(px_gpu, stream):
     # A 256-row f16 workgroup with Nq = 128 computes rows 128..255 from zero
     # queries but must not store them.

@@ -210,3 +210,41 @@ def test_gemm_fp16_operand_past_4gib(px_gpu, stream):
         assert np.abs(got - want[r % P]).max() / rms < 2e-2, r
     for b in (dA, dB, dC):
         b.free()
+
+
+# Every output of the BASELINE configs against the CPU's f32 GEMM (oracle
+# sgemm_f32, OpenMP; itself checked against the f64 oracle across its
+# blocking in test_oracle.py).  The sampled tests above hold the reference's
+# f64 points; these cover all 16.7 M outputs.
+def test_gemm_fp32_baseline_config_every_output(px_gpu, stream):
+    M = N = K = 4096
+    A = px_gpu.lcg_f32(1, M * K).reshape(M, K)
+    B = px_gpu.lcg_f32(2, K * N).reshape(K, N)
+    C = px_gpu.lcg_f32(3, M * N).reshape(M, N)
+    got = _gemm(px_gpu, stream, px_gpu.GEMM_FP32, A, B, C, 0.125, 1.5)
+    want = oracle.sgemm_f32(0.125, A, B, 1.5, C)
+    assert _norm_err(got, want) < 2e-5  # two f32 summation orders
+
+
+def test_gemm_fp16tc_baseline_config_every_output(px_gpu, stream):
+    A, B = _baseline_inputs(px_gpu)
+    C = np.zeros((4096, 4096), np.float32)
+    got = _gemm(px_gpu, stream, px_gpu.GEMM_FP16TC_FP32ACC, A, B, C, 1.0, 0.0)
+    want = oracle.sgemm_f32(1.0, A, B, 0.0, C)
+    assert np.abs(got - want).max() < 1e-4  # |C| ~ N(0,1): absolute = normalised
+
+
+def test_gemm_fp16_baseline_config_every_output(px_gpu, stream):
+    # both sides sum in f32 and round once to f16, so every output is within
+    # one f16 step (at either value) of the f32 oracle's rounded result, or,
+    # near zero where the two f32 sums' own rounding (~1e-7 here) exceeds
+    # the f16 step, within 1e-5 of the RMS
+    A, B = _baseline_inputs(px_gpu)
+    C = np.zeros((4096, 4096), np.float32)
+    got = _gemm(px_gpu, stream, px_gpu.GEMM_FP16, A, B, C, 1.0, 0.0, f16=True)
+    want = oracle.f16_round(oracle.sgemm_f32(1.0, A, B, 0.0, C))
+    assert _norm_err(got, want) < 2e-2
+    step = np.maximum(np.spacing(np.abs(want).astype(np.float16)),
+                      np.spacing(np.abs(got).astype(np.float16))).astype(np.float32)
+    bad = np.abs(got - want) > np.maximum(step, 1e-5 * np.sqrt(np.mean(want ** 2)))
+    assert not bad.any(), (int(bad.sum()), got[bad][:5], want[bad][:5])

@@ -270,6 +270,19 @@ def test_sgemm_baseline_agrees():
     assert np.allclose(got, want, rtol=1e-5, atol=1e-5)
 
 
+def test_sgemm_baseline_agrees_across_its_blocks():
+    # M, N and K each cross the CPU GEMM's 64 x 256 x 256 blocking, with a
+    # ragged last block: the full-size GPU checks use it as their checker
+    A = oracle.normal_f32(7, 130 * 600).reshape(130, 600)
+    B = oracle.normal_f32(8, 600 * 300).reshape(600, 300)
+    C = oracle.normal_f32(9, 130 * 300).reshape(130, 300)
+    got = oracle.sgemm_f32(0.75, A, B, -0.5, C)
+    want = oracle.gemm_full(A, B, C, 0.75, -0.5)
+    # f32 rounding of 600-term sums: a few 1e-6 of the RMS; a dropped or
+    # misplaced block would be O(1)
+    assert np.abs(got - want).max() / np.sqrt(np.mean(want ** 2)) < 2e-5
+
+
 def test_saxpy_mt_matches_scalar_saxpy():
     # the multi-core CPU baseline computes the same bits as the scalar oracle
     n = 1_000_003
