@@ -196,9 +196,13 @@ def test_misaligned_workspace_is_refused(px_gpu, bare_stream):
 def test_pod_split_compute_takes_an_arena_slab(px_gpu, tmp_path):
     # A 256 x 256 x 8192 gemm_fp32 COMPUTE (split 16 ways by the built-in
     # rule) in a pod: the tiles take 16.25 MiB of the arena and the split's
-    # partial sums another 4 MiB slab while the leaf runs; free device memory is the
-    # same before and after the segment.  With an arena too small for the
-    # slab the leaf runs unsplit, to the same bound.
+    # partial sums another 4 MiB slab while the leaf runs.  The COMPUTE runs
+    # in a segment of its own, between one that ALLOCs and LOADs its tiles
+    # and one that STOREs and FREEs them (tiles stay resident across
+    # segments), so free device memory can be read around it alone (LOAD and
+    # STORE stage through pinned host chunks the pod allocates as it needs
+    # them).  With an arena too small for the slab the leaf runs unsplit, to
+    # the same bound.
     from phobos_amd import cluster as cl
     px = px_gpu
     M, N, K = 256, 256, 8192
@@ -210,28 +214,66 @@ def test_pod_split_compute_takes_an_arena_slab(px_gpu, tmp_path):
     paths = [str(tmp_path / f) for f in ("a.bin", "b.bin", "c.bin", "out.bin")]
     for p, t in zip(paths, (a, b, c, c)):
         t.tofile(p)
-    seg = "\n".join([
+    load = "\n".join([
         f"1 - ALLOC 1 {M}x{K} f32", f"2 - ALLOC 2 {K}x{N} f32", f"3 - ALLOC 3 {M}x{N} f32",
-        f"4 1 LOAD 1 0 0,0 {M},{K}", f"5 2 LOAD 2 1 0,0 {K},{N}", f"6 3 LOAD 3 2 0,0 {M},{N}",
-        f"7 4,5,6 COMPUTE 1 1:r,2:r,3:rmw 3:f32:0x{px.f32_bits(alpha):08x},"
-        f"4:f32:0x{px.f32_bits(beta):08x} 4,4,1 256,1,1",
-        f"8 7 STORE 3 3 0,0 {M},{N}",
-        "9 8 FREE 1 0", "10 8 FREE 2 0", "11 8 FREE 3 0"]) + "\n"
+        f"4 1 LOAD 1 0 0,0 {M},{K}", f"5 2 LOAD 2 1 0,0 {K},{N}", f"6 3 LOAD 3 2 0,0 {M},{N}"]) + "\n"
+    compute = (f"1 - COMPUTE 1 1:r,2:r,3:rmw 3:f32:0x{px.f32_bits(alpha):08x},"
+               f"4:f32:0x{px.f32_bits(beta):08x} 4,4,1 256,1,1\n")
+    store = "\n".join([f"1 - STORE 3 3 0,0 {M},{N}", "2 1 FREE 1 0", "3 1 FREE 2 0",
+                       "4 1 FREE 3 0"]) + "\n"
     tiles = 4 * (M * K + K * N + M * N)
     for arena, split in ((tiles + need + (1 << 20), True), (tiles + (1 << 20), False)):
         pod = cl.Pod(arena, 2)
         for t, (p, shape) in enumerate(zip(paths, ((M, K), (K, N), (M, N), (M, N)))):
             pod.set_tensor(t, "file://" + p, shape)
         pod.set_kernel(1, px.GEMM_FP32)
-        pod.run(seg)  # warm: code objects, staging buffers
+        pod.run(load)
+        # warm both pod streams: the code objects load on first use, and a
+        # kernel that spills registers makes HIP grow the launch queue's
+        # scratch area on its first launch there (gemm_fp32's 256 x 256
+        # kernels spill outside their K loop)
+        pod.run(compute)
+        pod.run(compute)
+        pod.run(store)
+        pod.run(load)
         with _NoGc():
             before = _free_bytes()
-            st = pod.run(seg)
+            st = pod.run(compute)
             assert _free_bytes() == before
         assert st["compute"] == 1
         bump = pod.arena_stats()[1]
         assert (bump >= tiles + need) == split, (bump, tiles, need)
+        pod.run(store)
         got = np.fromfile(paths[3], np.float32).reshape(M, N)
         rel = np.abs(got - want) / np.maximum(np.abs(want), 1e-2 * np.sqrt(np.mean(want ** 2)))
         assert rel.max() < 1e-4, (split, rel.max())
         pod.close()
+
+
+def test_two_streams_with_their_own_workspaces(px_gpu):
+    # split launches on two streams at once, each stream with its own bound
+    # workspace: ten interleaved rounds, every result equal to the first
+    px = px_gpu
+    s1, s2 = px.Stream(), px.Stream()
+    try:
+        sp, need = px.split_plan(px.FLASH_FP16, [4096, 4096, 64])
+        assert sp > 1
+        w1, w2 = px.DeviceBuffer(need), px.DeviceBuffer(need)
+        px.set_workspace(s1, w1.ptr, need)
+        px.set_workspace(s2, w2.ptr, need)
+        l1, c1, k1 = _one_head_flash(px, s1, seed=101)
+        l2, c2, k2 = _one_head_flash(px, s2, seed=201)
+        l1()
+        l2()
+        s1.synchronize()
+        s2.synchronize()
+        first1, first2 = c1(), c2()
+        for _ in range(10):
+            l1()
+            l2()
+        s1.synchronize()
+        s2.synchronize()
+        assert np.array_equal(c1(), first1) and np.array_equal(c2(), first2)
+    finally:
+        s1.destroy()
+        s2.destroy()
