@@ -248,3 +248,25 @@ def test_gemm_fp16_baseline_config_every_output(px_gpu, stream):
                       np.spacing(np.abs(got).astype(np.float16))).astype(np.float32)
     bad = np.abs(got - want) > np.maximum(step, 1e-5 * np.sqrt(np.mean(want ** 2)))
     assert not bad.any(), (int(bad.sum()), got[bad][:5], want[bad][:5])
+
+
+@pytest.mark.parametrize("M,N,K", [(128, 128, 32), (256, 384, 96), (512, 256, 1024), (300, 200, 100)])
+def test_gemm_fp32_small_strict_relative(px_gpu, stream, M, N, K):
+    # non-negative operands and scalars: no output cancels, so every output
+    # is held to BASELINE's 1e-4 relative error with the reference's own
+    # floor, f64::MIN_POSITIVE (main.rs:398-402), at the built-in plan and at
+    # every tiling
+    px = px_gpu
+    A = np.abs(oracle.lcg_f32(11, M * K)).reshape(M, K)
+    B = np.abs(oracle.lcg_f32(12, K * N)).reshape(K, N)
+    C = np.abs(oracle.lcg_f32(13, M * N)).reshape(M, N)
+    want = oracle.gemm_full(A, B, C, 0.125, 1.5)
+    for variant in [None] + list(range(8)):
+        if variant is not None:
+            px.plan_pin(px.GEMM_FP32, [M, N, K], 1, variant)
+        try:
+            got = _gemm(px, stream, px.GEMM_FP32, A, B, C, 0.125, 1.5)
+        finally:
+            px.plan_pin(px.GEMM_FP32, [M, N, K], None)
+        rel = np.abs(got - want) / np.maximum(np.abs(want), np.finfo(np.float64).tiny)
+        assert rel.max() < 1e-4, (variant, rel.max())
