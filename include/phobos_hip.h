@@ -276,11 +276,13 @@ int phx_arena_stats(phx_arena a, size_t *cap, size_t *bump, uint64_t *base);
  * the reference: it is for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc).  Same arguments, split plan, kernels and results (bit for bit)
- * as phx_flash_attention_bh; a launch split over the keys keeps its partial
- * results in a fixed PHX_SCRATCH_BYTES (16 MiB) device array that the library
- * holds on each initialised GPU until the process ends, instead of a pool
- * workspace.  A split that needs more scratch (phx_split_plan) returns
- * PHX_E_INVALID; phx_flash_attention_bh takes any size.  Every call on a GPU
+ * as phx_flash_attention_bh on a stream whose bound workspace holds the
+ * split; a launch split over the keys keeps its partial results in a fixed
+ * PHX_SCRATCH_BYTES (16 MiB) device array that the library holds on each
+ * initialised GPU until the process ends, instead of the stream's workspace
+ * (it splits whether or not one is bound).  A split that needs more
+ * scratch (phx_split_plan) returns PHX_E_INVALID; phx_flash_attention_bh
+ * takes any size.  Every call on a GPU
  * shares that GPU's array: calls that overlap on one GPU (several streams or
  * threads) race. */
 int phx_flash_attention_bh_noalloc(phx_stream s, phx_kernel k, uint64_t q, uint64_t kk,

@@ -3,10 +3,12 @@
 // loops, harnesses that forbid hipMalloc.  It has no counterpart in the
 // reference.
 //
-// phx_flash_attention_bh splits small launches over the keys and takes the
-// split's workspace (partial accumulators, running maxima and row sums) from
-// HIP's stream-ordered pool.  This entry point runs the same plan and the
-// same kernels, with the workspace in a fixed array of PHX_SCRATCH_BYTES
+// phx_flash_attention_bh splits small launches over the keys when the
+// caller has bound a workspace to the launch stream (phx_stream_set_workspace)
+// for the split's partial accumulators, running maxima and row sums, and
+// runs unsplit otherwise.  This entry point runs the built-in split plan and
+// the same kernels whether or not a workspace is bound, with the workspace
+// in a fixed array of PHX_SCRATCH_BYTES
 // device memory that the library holds on each GPU it is initialised on,
 // until the process ends.  Every call on a GPU shares that GPU's array:
 // calls that overlap on one GPU (on different streams, or from several

@@ -1,7 +1,8 @@
 """phx_flash_attention_bh_noalloc: the allocation-free variant of
-phx_flash_attention_bh (a fixed device scratch array instead of a workspace
-from HIP's memory pool), called through the C ABI and checked bit for bit
-against the existing entry point: same split plan, same kernels, so the
+phx_flash_attention_bh (a fixed device scratch array instead of the
+workspace bound to the stream), called through the C ABI and checked bit for
+bit against the existing entry point on the session stream, whose bound
+workspace holds every split here: same split plan, same kernels, so the
 outputs must be identical.  Two calls in a row, the second smaller, so the
 second runs on scratch the first left behind; a size whose split needs more
 than the scratch holds is refused; an unsplit size runs the batched kernel."""
