@@ -103,7 +103,8 @@ int phx_stream_synchronize(phx_stream s);
  * engine.rs:582-647) for the split launches of this backend.  A built-in
  * GEMM or flash launch that phx_split_plan would split runs with the largest
  * split whose workspace fits in the bound bytes, and unsplit when none fits
- * or nothing is bound; it never allocates.  The buffer must stay valid until
+ * or nothing is bound (gemm_fp32 without a pin then takes its 64 x 64 x 16
+ * tiling, which needs no workspace); it never allocates.  The buffer must stay valid until
  * every launch on s that may use it has completed; launches on one stream
  * run in order, so they can share it.  Unbinding (or phx_stream_destroy)
  * forgets it; the caller frees it. */

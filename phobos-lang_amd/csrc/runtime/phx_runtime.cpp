@@ -355,11 +355,11 @@ struct PlanKeyHash {
 std::mutex g_plan_mu;
 std::unordered_map<PlanKey, phx_plan, PlanKeyHash> g_plans;
 
-bool pinned_plan(const PlanKey &key, phx_plan *out) {
+bool pinned_plan(const PlanKey &key, phx_plan *out) {  // out may be null
     std::lock_guard<std::mutex> lock(g_plan_mu);
     auto it = g_plans.find(key);
     if (it == g_plans.end()) return false;
-    *out = it->second;
+    if (out) *out = it->second;
     return true;
 }
 bool is_gemm(phx_kernel k) {
@@ -635,6 +635,13 @@ int launch_raw(hipFunction_t f, const uint32_t grid[3], const uint32_t block[3],
             if (int rc = check_shape((phx_kernel)k, d, nd)) return rc;
             const Workspace w = stream_workspace(s);
             const int sp = gemm_split_fit((phx_kernel)k, d[0], d[1], d[2], w.bytes);
+            // gemm_fp32's built-in plan split over K, but the stream has no
+            // workspace for it: the 64 x 64 tiling fills the GPU without one
+            // (256^2 x 8192: 151 us against 1.8 ms for one 256 x 256 tile)
+            const bool no_room = k == PHX_GEMM_FP32 && sp == 1 &&
+                                 gemm_split((phx_kernel)k, d[0], d[1], d[2]) > 1 &&
+                                 !pinned_plan(gemm_key((phx_kernel)k, d[0], d[1], d[2]), nullptr) &&
+                                 !getenv("PHX_GEMM_SPLIT");
             if (sp > 1) {
                 float alpha, beta;  // the two f32 scalars after the three memrefs
                 memcpy(&alpha, args[21], 4);
@@ -643,7 +650,8 @@ int launch_raw(hipFunction_t f, const uint32_t grid[3], const uint32_t block[3],
                                             s, w.ptr);
             }
             if (k == PHX_GEMM_FP32) {
-                if (const int v = s32_variant(d[0], d[1], d[2])) {
+                const int v = no_room ? PHX_S32_SMALL_VARIANT : s32_variant(d[0], d[1], d[2]);
+                if (v) {
                     const S32Tiling &ti = kS32[v];
                     hipFunction_t fv;
                     if (int rc = aux_function(kSpecs[k].file, ti.entry, &fv)) return rc;

@@ -153,13 +153,23 @@ def test_reference_flash_launch_splits_inside_the_bound_workspace(px_gpu, bare_s
     assert px.get_workspace(s) == (0, 0)
 
 
-def test_unbound_stream_runs_unsplit_and_allocates_nothing(px_gpu, bare_stream):
+def test_unbound_stream_runs_without_a_split_and_allocates_nothing(px_gpu, bare_stream):
+    # the flash launch runs unsplit; the gemm_fp32 launch (whose built-in
+    # plan splits 16 ways) runs its 64 x 64 tiling, which needs no workspace
     px, s = px_gpu, bare_stream
     assert px.get_workspace(s) == (0, 0)
     launch, check, _ = _one_head_flash(px, s, seed=15)
     _run_checked(px, s, launch, check)
     glaunch, gcheck, _ = _gemm_fp32_compute(px, s, seed=21)
     _run_checked(px, s, glaunch, gcheck)
+    # one 256 x 256 tile would take about 1.8 ms; the 64 x 64 tiling about 0.15
+    e0, e1 = px.Event(), px.Event()
+    e0.record(s)
+    for _ in range(3):
+        glaunch()
+    e1.record(s)
+    e1.synchronize()
+    assert e0.elapsed_ms(e1) / 3 < 0.8
 
 
 def test_gemm_compute_splits_inside_the_bound_workspace(px_gpu, bare_stream):
