@@ -74,6 +74,28 @@ def test_random_gemm_shapes(px_gpu, stream, name):
         assert err < (1e-5 if name == "GEMM_FP32" else 1e-4 if not f16 else 2e-2), (M, N, K, err)
 
 
+@pytest.mark.parametrize("variant", range(1, 8))
+def test_random_gemm_fp32_tiling_shapes(px_gpu, stream, variant):
+    # every other gemm_fp32 tiling (TILE_M x TILE_N x TILE_K), pinned, over
+    # 12 seeded shapes of the contract, a guard after C, the gemm_fp32 bound
+    px = px_gpu
+    for i, (M, N, K, alpha, beta, _) in enumerate(_cases("GEMM_FP32", 12 + variant)[variant:]):
+        px.plan_pin(px.GEMM_FP32, [M, N, K], 1, variant)
+        A = oracle.normal_f32(400 + i, M * K, 1 / np.sqrt(K)).reshape(M, K)
+        B = oracle.normal_f32(500 + i, K * N, 1 / np.sqrt(K)).reshape(K, N)
+        C = oracle.normal_f32(600 + i, M * N).reshape(M, N)
+        c = np.concatenate([C.ravel(), np.full(GUARD, SENTINEL, np.float32)])
+        da, db, dc = (px.DeviceBuffer.from_array(np.ascontiguousarray(t)) for t in (A, B, c))
+        print(f"tiling {px.GEMM_FP32_TILINGS[variant]} M={M} N={N} K={K}", flush=True)
+        px.launch_gemm(stream, px.GEMM_FP32, da, db, dc, M, N, K, alpha, beta)
+        stream.synchronize()
+        raw = dc.download(np.float32, M * N + GUARD)
+        assert np.array_equal(raw[M * N:], c[M * N:]), f"store past C at {(M, N, K)}"
+        want = oracle.gemm_full(A, B, C, alpha, beta)
+        err = np.abs(raw[:M * N].reshape(M, N) - want).max() / np.sqrt(np.mean(want ** 2))
+        assert err < 1e-5, (variant, M, N, K, err)
+
+
 @pytest.mark.parametrize("bits", [16, 32])
 def test_random_flash_shapes(px_gpu, stream, bits):
     px = px_gpu
