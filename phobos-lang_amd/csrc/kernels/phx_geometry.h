@@ -39,19 +39,35 @@
 #define PHX_S_NK_MULT 4
 
 // Split-K (gemm_fp32, gemm_fp16tc_fp32acc, gemm_fp16): when a GEMM has
-// fewer than PHX_SPLIT_MIN_TILES output tiles, its K range is cut into
-// chunks of whole 32-deep steps computed by separate workgroups
+// fewer than PHX_SPLIT_MIN_TILES output tiles of 256 x 256, its K range is
+// cut into chunks of whole 32-deep steps computed by separate workgroups
 // (gemm_splitk), whose f32 partial sums gemm_splitk_reduce adds in a fixed
-// order.  At most PHX_SPLIT_MAX chunks, each of at least
-// PHX_SPLIT_MIN_STEPS_F32 (gemm_fp32) or PHX_SPLIT_MIN_STEPS_F16 (the f16
-// MFMA GEMMs, whose K steps are 8x cheaper) 32-deep steps: measured on
-// MI355X at 512^3 .. 2048^3 and 256^2 x 16384, shorter f16 chunks lose more
-// to the partial-sum traffic than they gain.
+// order.  gemm_fp32 aims at PHX_SPLIT_TARGET_F32 workgroups with chunks of
+// at least PHX_SPLIT_MIN_STEPS_F32 steps; the f16 MFMA GEMMs, whose K steps
+// are 8x cheaper, at PHX_SPLIT_TARGET_F16 workgroups with chunks of at least
+// PHX_SPLIT_MIN_STEPS_F16 steps, or PHX_SPLIT_MIN_STEPS_F16_WIDE once a
+// launch has PHX_SPLIT_WIDE_TILES tiles; at most PHX_SPLIT_MAX chunks.
+// Measured on MI355X with the partial sums in a workspace the caller bound
+// (HIP events, pinned split counts): gemm_fp16 512^3 16.6 us unsplit, 14.0
+// at 2 chunks; 768^3 20.4 / 17.1 at 3; 1536^3 33.8 / 25.8 at 3; 512^2 x
+// 2048 38.2 / 18.6 at 8; 256^2 x 4096 67.5 / 18.0 at 16; 2048^3 42.6 / 36.5
+// at 2; and at 2048^2 x 1024 the split loses (26.5 / 28.5 at 2), as it does
+// at 3072^2 x 1024 (31.5 / 53.8); gemm_fp16tc_fp32acc alike.
+#define PHX_SPLIT_MIN_TILES 128
+#define PHX_SPLIT_MAX 16
+#define PHX_SPLIT_TARGET_F32 256
+#define PHX_SPLIT_TARGET_F16 128
+#define PHX_SPLIT_MIN_STEPS_F32 1
+#define PHX_SPLIT_MIN_STEPS_F16 8
+#define PHX_SPLIT_MIN_STEPS_F16_WIDE 32
+#define PHX_SPLIT_WIDE_TILES 64
+#define PHX_SPLIT_KSTEP 32
+
 // gemm_fp32's built-in tiling (no pin): 256 x 256 x 16 when its tiles fill
 // all PHX_S32_FULL_TILES CUs; else 64 x 64 x 16 (launch-plan variant
 // PHX_S32_SMALL_VARIANT) when that gives at least PHX_S32_SMALL_MIN_TILES
 // tiles, or at least PHX_S32_SMALL_SHORT_TILES with K <= PHX_S32_SHORT_K;
-// else the split rule below.  Measured on MI355X (one box, HIP events): the
+// else the split rule above.  Measured on MI355X (one box, HIP events): the
 // small tile beats both the 256 x 256 tile and its split at 3072^2 x 1024
 // (151 vs 260 us unsplit), 2048^3 (133 vs 160 split), 768^3 (18.5 vs 44),
 // 1024^2 x 256 (9 vs 40) and 512^2 x 2048 (41 vs 58); the split stays ahead
@@ -63,11 +79,6 @@
 #define PHX_S32_SMALL_SHORT_TILES 16
 #define PHX_S32_SHORT_K 4096
 
-#define PHX_SPLIT_MIN_TILES 128
-#define PHX_SPLIT_MAX 16
-#define PHX_SPLIT_MIN_STEPS_F32 1
-#define PHX_SPLIT_MIN_STEPS_F16 32
-#define PHX_SPLIT_KSTEP 32
 #define PHX_REDUCE_THREADS 256
 
 // Split keys (flash attention): when the (query block, head) work items

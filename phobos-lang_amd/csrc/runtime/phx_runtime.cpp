@@ -459,8 +459,8 @@ static int s32_variant(int64_t M, int64_t N, int64_t K) {
 
 // How many K chunks a GEMM is split into (1: no split).  A GEMM whose
 // 256 x 256 output tiles cannot fill half of the 256 CUs gets enough chunks
-// to give every CU a workgroup, within the chunk-length floor of its kernel
-// and at most PHX_SPLIT_MAX chunks.  PHX_GEMM_SPLIT=<n> in the environment
+// to give its kernel's target number of workgroups, within its chunk-length
+// floor and at most PHX_SPLIT_MAX chunks (phx_geometry.h).  PHX_GEMM_SPLIT=<n> in the environment
 // forces n (1 turns the split off), for measurement.
 int gemm_split(phx_kernel k, int64_t M, int64_t N, int64_t K) {
     const int64_t tiles = ((M + PHX_H_BM - 1) / PHX_H_BM) * ((N + PHX_H_BN - 1) / PHX_H_BN);
@@ -474,9 +474,11 @@ int gemm_split(phx_kernel k, int64_t M, int64_t N, int64_t K) {
     } else {
         if (k == PHX_GEMM_FP32 && s32_rule(M, N, K) != 0) return 1;  // a smaller tile instead
         if (tiles >= PHX_SPLIT_MIN_TILES) return 1;
-        const int64_t min_steps =
-            k == PHX_GEMM_FP32 ? PHX_SPLIT_MIN_STEPS_F32 : PHX_SPLIT_MIN_STEPS_F16;
-        sp = 256 / tiles;
+        const bool f32 = k == PHX_GEMM_FP32;
+        const int64_t min_steps = f32                            ? PHX_SPLIT_MIN_STEPS_F32
+                                  : tiles >= PHX_SPLIT_WIDE_TILES ? PHX_SPLIT_MIN_STEPS_F16_WIDE
+                                                                  : PHX_SPLIT_MIN_STEPS_F16;
+        sp = (f32 ? PHX_SPLIT_TARGET_F32 : PHX_SPLIT_TARGET_F16) / tiles;
         if (sp > steps / min_steps) sp = steps / min_steps;
         if (sp > PHX_SPLIT_MAX) sp = PHX_SPLIT_MAX;
     }

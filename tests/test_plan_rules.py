@@ -2,8 +2,9 @@
 phx_plan_pin) on the CPU: they are host logic, so no device is needed.  The
 split rule is restated here independently (phx_geometry.h's constants:
 256 x 256 output tiles, 32-deep K steps, at least 128 tiles or 256 of 512
-flash slots before anything splits, at most 16 chunks, at least 1 K step per
-chunk for gemm_fp32 and 32 for the f16 GEMMs, at least 8 key blocks per flash
+flash slots before anything splits, at most 16 chunks, aiming at 256
+workgroups with at least 1 K step per chunk for gemm_fp32 and at 128 with at
+least 8 (32 from 64 tiles up) for the f16 GEMMs, at least 8 key blocks per flash
 chunk, no empty chunk; gemm_fp32 takes its 64 x 64 x 16 tiling instead of a
 split below 256 tiles of 256 x 256 when that gives at least 128 tiles, or 16
 with K <= 4096) and compared over a grid of shapes."""
@@ -44,7 +45,11 @@ def _gemm_rule(kern, M, N, K):
         return 1
     if tiles >= 128:
         return 1
-    sp = min(256 // tiles, steps // (1 if kern == px.GEMM_FP32 else 32), 16)
+    if kern == px.GEMM_FP32:
+        target, min_steps = 256, 1
+    else:
+        target, min_steps = 128, (32 if tiles >= 64 else 8)
+    sp = min(target // tiles, steps // min_steps, 16)
     return _rounded(steps, sp)
 
 
