@@ -83,15 +83,25 @@
 
 // Split keys (flash attention): when the (query block, head) work items
 // cannot fill half of the PHX_FA_SLOTS workgroup slots (256 CUs x 2
-// resident workgroups), the keys are cut into chunks of whole 64-key blocks,
-// at least PHX_FLASH_SPLIT_MIN_BLOCKS each and at most PHX_SPLIT_MAX chunks,
+// resident workgroups), the keys are cut into chunks of whole 64-key blocks
 // run as separate workgroups (flash_attention_split) and merged by
-// flash_combine.
+// flash_combine: enough chunks for PHX_FLASH_SPLIT_TARGET workgroups, of at
+// least PHX_FLASH_SPLIT_MIN_BLOCKS_F16 (f16) or _F32 (f32) blocks each, at
+// most PHX_SPLIT_MAX.  Measured on MI355X with the partial results in a
+// workspace the caller bound (HIP events, pinned chunk counts; best count
+// in brackets): f16 one head 1024^2 14.3 us (6) against 17.7 at the
+// earlier rule's 2; 8192^2 34.4 (8) against 39.4 at 16; 4 heads 4096^2 32.2
+// (4) against 36.3 at 8; f32 one head 1024^2 19.5 (8) against 41.2 at 2,
+// 2048^2 27.0 (16) against 43.2 at 4.  One workgroup per CU (256) beat
+// filling both slots of every CU, and short chunks beat the earlier floor of
+// 8 blocks, whose tuning had a workspace allocation in every split launch.
 #define PHX_FA_SLOTS 512
+#define PHX_FLASH_SPLIT_TARGET 256
+#define PHX_FLASH_SPLIT_MIN_BLOCKS_F16 5
+#define PHX_FLASH_SPLIT_MIN_BLOCKS_F32 2
 // Device bytes of the fixed scratch array behind the allocation-free flash
 // entry point (phx_flash_attention_bh_noalloc): its split-key workspace.
 #define PHX_SCRATCH_BYTES (16u << 20)
-#define PHX_FLASH_SPLIT_MIN_BLOCKS 8
 
 // matmul_init: element-wise, 256 threads x 4 float4.
 #define PHX_EW_THREADS 256

@@ -565,8 +565,10 @@ int flash_split(phx_kernel k, int64_t BH, int64_t Nq, int64_t Nk) {
         sp = pin.splits;
     } else {
         if (2 * items >= PHX_FA_SLOTS) return 1;
-        sp = PHX_FA_SLOTS / items;
-        if (sp > nkb / PHX_FLASH_SPLIT_MIN_BLOCKS) sp = nkb / PHX_FLASH_SPLIT_MIN_BLOCKS;
+        const int64_t min_blocks =
+            flash_f16(k) ? PHX_FLASH_SPLIT_MIN_BLOCKS_F16 : PHX_FLASH_SPLIT_MIN_BLOCKS_F32;
+        sp = PHX_FLASH_SPLIT_TARGET / items;
+        if (sp > nkb / min_blocks) sp = nkb / min_blocks;
         if (sp > PHX_SPLIT_MAX) sp = PHX_SPLIT_MAX;
     }
     return round_split(nkb, sp);  // whole blocks per chunk; no empty chunk

@@ -4,8 +4,9 @@ split rule is restated here independently (phx_geometry.h's constants:
 256 x 256 output tiles, 32-deep K steps, at least 128 tiles or 256 of 512
 flash slots before anything splits, at most 16 chunks, aiming at 256
 workgroups with at least 1 K step per chunk for gemm_fp32 and at 128 with at
-least 8 (32 from 64 tiles up) for the f16 GEMMs, at least 8 key blocks per flash
-chunk, no empty chunk; gemm_fp32 takes its 64 x 64 x 16 tiling instead of a
+least 8 (32 from 64 tiles up) for the f16 GEMMs; flash aiming at 256
+workgroups with at least 5 (f16) or 2 (f32) key blocks per chunk; no empty
+chunk; gemm_fp32 takes its 64 x 64 x 16 tiling instead of a
 split below 256 tiles of 256 x 256 when that gives at least 128 tiles, or 16
 with K <= 4096) and compared over a grid of shapes."""
 import itertools
@@ -58,7 +59,7 @@ def _flash_rule(f16, BH, Nq, Nk):
     nkb = -(-Nk // 64)
     if 2 * items >= 512:
         return 1
-    return _rounded(nkb, min(512 // items, nkb // 8, 16))
+    return _rounded(nkb, min(256 // items, nkb // (5 if f16 else 2), 16))
 
 
 GEMMS = ["GEMM_FP32", "GEMM_FP16TC_FP32ACC", "GEMM_FP16"]
