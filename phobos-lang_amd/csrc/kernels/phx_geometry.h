@@ -89,7 +89,7 @@
 // least PHX_FLASH_SPLIT_MIN_BLOCKS_F16 (f16) or _F32 (f32) blocks each, at
 // most PHX_SPLIT_MAX.  Measured on MI355X with the partial results in a
 // workspace the caller bound (HIP events, pinned chunk counts; best count
-// in brackets): f16 one head 1024^2 14.3 us (6) against 17.7 at the
+// in brackets): f16 one head 1024^2 16.2 us (3; 14.3 at 6) against 17.7 at the
 // earlier rule's 2; 8192^2 34.4 (8) against 39.4 at 16; 4 heads 4096^2 32.2
 // (4) against 36.3 at 8; f32 one head 1024^2 19.5 (8) against 41.2 at 2,
 // 2048^2 27.0 (16) against 43.2 at 4.  One workgroup per CU (256) beat
