@@ -168,3 +168,23 @@ def test_rust_ffi_stub_matches_header():
           for n, p in re.findall(r"pub fn (phx_\w+)\(([^)]*)\)", block)}
     assert len(decls) >= 60
     assert rs == decls
+
+
+def test_stream_workspace_binding_is_host_logic():
+    # phx_stream_set_workspace / _get_workspace keep a per-stream table and
+    # touch no device: bind, rebind, unbind, per-stream isolation and the
+    # alignment check, with stream handles that are only keys here
+    s1, s2 = 0x1000, 0x2000
+    px.set_workspace(s1, 1 << 20, 4096)
+    px.set_workspace(s2, 2 << 20, 8192)
+    assert px.get_workspace(s1) == (1 << 20, 4096)
+    assert px.get_workspace(s2) == (2 << 20, 8192)
+    px.set_workspace(s1, 3 << 20, 256)
+    assert px.get_workspace(s1) == (3 << 20, 256)
+    px.set_workspace(s1, 0, 0)
+    assert px.get_workspace(s1) == (0, 0) and px.get_workspace(s2) == (2 << 20, 8192)
+    px.set_workspace(s2, 2 << 20, 0)  # zero bytes unbinds too
+    assert px.get_workspace(s2) == (0, 0)
+    with pytest.raises(px.PhxError, match="256-byte aligned"):
+        px.set_workspace(s1, (1 << 20) + 128, 4096)
+    assert px.get_workspace(s1) == (0, 0)
