@@ -307,9 +307,17 @@ int phx_f16_to_f32(size_t n, const uint16_t *in, float *out);
 /* ------------------------------------------------------------ pod segment */
 /* One-pod executor for ALLOC/LOAD/COMPUTE/STORE/FREE segments
  * (Engine, phobos-pod/src/engine.rs:121-232, 355-398, 424-509).  The segment
- * is given in the text form documented in INTEGRATION.md; kernels are the
- * built-in ids or functions bound with phx_pod_set_kernel_function.  LOAD/STORE use file:// f32 tensors (storage.rs:22-79) staged
- * through pinned host buffers with async copies. */
+ * is text, one instruction per line ('#' starts a comment), the fields of
+ * phobos_v1_isa.proto / isa.rs:25-50:
+ *   <iid> <deps|-> ALLOC   <tile> <d0xd1> f32
+ *   <iid> <deps>   LOAD    <tile> <tensor> <off0,off1> <s0,s1>
+ *   <iid> <deps>   COMPUTE <kernel> <tile:r|w|rmw,...> <pos:f32:0xBITS,...|-> <gx,gy,gz> <cx,cy,cz>
+ *   <iid> <deps>   STORE   <tile> <tensor> <off0,off1> <s0,s1>
+ *   <iid> <deps>   FREE    <tile> <expected_serves>
+ * (deps: comma-separated iids; phx_segment_pb_to_text writes this form from
+ * a wire Segment).  Kernels are the built-in ids or functions bound with
+ * phx_pod_set_kernel_function.  LOAD/STORE use file:// f32 tensors
+ * (storage.rs:22-79) staged through pinned host buffers with async copies. */
 typedef struct phx_pod_s *phx_pod;
 int phx_pod_create(phx_pod *p, size_t arena_bytes, int nstreams);
 int phx_pod_destroy(phx_pod p);

@@ -152,7 +152,7 @@ def test_calls_before_init_fail_loudly():
 
 
 def test_rust_ffi_stub_matches_header():
-    # INTEGRATION.md's phobos-hip-sys block (the binding the reference's
+    # The integration notes' phobos-hip-sys block (the binding the reference's
     # Rust side would add) declares every function of include/phobos_hip.h
     # with the same number of parameters.
     import re
