@@ -287,3 +287,55 @@ def test_two_streams_with_their_own_workspaces(px_gpu):
     finally:
         s1.destroy()
         s2.destroy()
+
+
+@pytest.mark.parametrize("slabs", [6, 2])
+def test_pod_concurrent_split_computes_each_take_a_slab(px_gpu, tmp_path, slabs):
+    # six independent split gemm_fp32 COMPUTEs (256 x 256 x 8192, one C tile
+    # each) on a pod's four streams: each leaf binds its own arena slab to its
+    # stream for its launch.  With room for all six slabs every leaf splits;
+    # with room for two, the others find the arena full and run unsplit on
+    # the 256 x 256 tiling.  Every C matches the oracle either way.
+    from phobos_amd import cluster as cl
+    px = px_gpu
+    M, N, K, n = 256, 256, 8192, 6
+    alpha, beta = 0.5, -1.0
+    sp, need = px.split_plan(px.GEMM_FP32, [M, N, K])
+    assert sp > 1
+    a = oracle.lcg_f32(71, M * K)
+    b = oracle.lcg_f32(72, K * N)
+    cs = [oracle.lcg_f32(80 + i, M * N) for i in range(n)]
+    paths = [str(tmp_path / "a.bin"), str(tmp_path / "b.bin")] + \
+        [str(tmp_path / f"c{i}.bin") for i in range(n)]
+    a.tofile(paths[0])
+    b.tofile(paths[1])
+    for i in range(n):
+        cs[i].tofile(paths[2 + i])
+    lines = [f"1 - ALLOC 1 {M}x{K} f32", f"2 - ALLOC 2 {K}x{N} f32",
+             f"3 1 LOAD 1 0 0,0 {M},{K}", f"4 2 LOAD 2 1 0,0 {K},{N}"]
+    sc = f"3:f32:0x{px.f32_bits(alpha):08x},4:f32:0x{px.f32_bits(beta):08x}"
+    iid = 5
+    frees = []
+    for i in range(n):
+        t = 10 + i
+        lines += [f"{iid} - ALLOC {t} {M}x{N} f32", f"{iid + 1} {iid} LOAD {t} {2 + i} 0,0 {M},{N}",
+                  f"{iid + 2} 3,4,{iid + 1} COMPUTE 1 1:r,2:r,{t}:rmw {sc} 1,1,1 256,1,1",
+                  f"{iid + 3} {iid + 2} STORE {t} {2 + i} 0,0 {M},{N}",
+                  f"{iid + 4} {iid + 3} FREE {t} 0"]
+        frees.append(str(iid + 2))
+        iid += 5
+    lines += [f"{iid} {','.join(frees)} FREE 1 0", f"{iid + 1} {','.join(frees)} FREE 2 0"]
+    tiles = 4 * (M * K + K * N + n * M * N)
+    pod = cl.Pod(tiles + slabs * need + (1 << 20), 4)
+    for t, (p, shape) in enumerate(zip(paths, [(M, K), (K, N)] + [(M, N)] * n)):
+        pod.set_tensor(t, "file://" + p, shape)
+    pod.set_kernel(1, px.GEMM_FP32)
+    st = pod.run("\n".join(lines) + "\n")
+    assert st["compute"] == n
+    A, B = a.reshape(M, K), b.reshape(K, N)
+    for i in range(n):
+        got = np.fromfile(paths[2 + i], np.float32).reshape(M, N)
+        want = oracle.gemm_full(A, B, cs[i].reshape(M, N), alpha, beta)
+        rel = np.abs(got - want) / np.maximum(np.abs(want), 1e-2 * np.sqrt(np.mean(want ** 2)))
+        assert rel.max() < 1e-4, (slabs, i, rel.max())
+    pod.close()
