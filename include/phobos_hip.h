@@ -189,8 +189,9 @@ int phx_split_plan(phx_kernel k, const int64_t *dims, int ndims, int *splits,
  *            2 128x256x16, 3 128x128x16, 4 128x128x32, 5 128x128x8,
  *            6 256x256x8, 7 64x64x16 (code object entries "gemm" and
  *            "gemm_t<M>x<N>k<K>");
- *            gemm_fp16tc_fp32acc on whole 256 x 256 tiles: 0 the eight-wave
- *            kernel, 1 the one-wave kernel; 0 for every other kernel.
+ *            gemm_fp16tc_fp32acc: 0 the eight-wave kernels (entries
+ *            "gemm_w8", "gemm_w8_splitk"), 1 the one-wave kernels ("gemm",
+ *            "gemm_splitk"), split or not; 0 for every other kernel.
  * A launch uses the plan pinned for its kernel and dims, else the built-in
  * rule.  The PHX_GEMM_SPLIT, PHX_FLASH_SPLIT and PHX_GEMM_W8 environment
  * variables, which force a plan for measurement, take precedence over both. */

@@ -728,8 +728,8 @@ extern "C" __global__ __launch_bounds__(256) void gemm_splitk_reduce(const float
 
 #ifdef PHX_GEMM_TC
 // ------------------------------------------------- eight-wave tc kernel
-// gemm_w8: the whole-tile gemm_fp16tc_fp32acc (M, N multiples of 256, K of
-// 32) with two waves per SIMD.  The one-wave-per-SIMD kernel above issues
+// gemm_w8 / gemm_w8_splitk: gemm_fp16tc_fp32acc with two waves per SIMD,
+// at every shape the one-wave kernels take (ragged edges masked as there).  The one-wave-per-SIMD kernel above issues
 // its f32 operand loads and its MFMAs from one instruction stream; when the
 // CU's load path is saturated (64 KiB of f32 per K step, as many cycles as
 // the step's MFMAs) a load that cannot issue holds up the MFMAs behind it,
@@ -774,11 +774,49 @@ __device__ __forceinline__ void w8_mfma(phx_f16v (&acc)[4][2], const Frags8 &f, 
 // C = fl(fl(alpha*acc) + fl(beta*c)) over a wave's 128 x 64 block at (r0,
 // c0), rounded once to the output type; C is not read when beta == 0.  Lane
 // l holds column 32j + l%32 and rows 32i + 8(r/4) + 4(l/32) + r%4; a store
-// writes two row segments of 32 elements.
-__device__ __forceinline__ void w8_epilogue(const phx_f16v (&acc)[4][2], TOut *C, int64_t ldc,
-                                            uint32_t r0, uint32_t c0, float alpha, float beta,
-                                            uint32_t lane) {
+// writes two row segments of 32 elements.  RG: C is read and written
+// through a buffer resource over the block's rows that exist, and a lane
+// whose column lies past N gets an out-of-range column offset (as in the
+// one-wave epilogue: no per-store test).
+template <bool RG, typename TO>
+__device__ __forceinline__ void w8_epilogue(const phx_f16v (&acc)[4][2], TO *C, int64_t ldc,
+                                            int64_t M, int64_t N, uint32_t r0, uint32_t c0,
+                                            float alpha, float beta, uint32_t lane) {
+    static_assert(sizeof(TO) == 4, "gemm_w8 stores f32");
     const uint32_t lrow = 4 * (lane >> 5), lcol = lane & 31;
+    if constexpr (RG) {
+        if ((int64_t)r0 >= M) return;  // the whole block lies past M (uniform)
+        const uint32_t ml = (uint32_t)(M - r0);
+        const uint32_t rows = ml < W8_WM ? ml : W8_WM;
+        const uint32_t pitch = (uint32_t)ldc * (uint32_t)sizeof(TO);
+        const __amdgpu_buffer_rsrc_t rc = phx_rsrc(C + (int64_t)r0 * ldc, rows * pitch);
+        uint32_t vo[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const uint32_t col = c0 + 32 * j + lcol;
+            vo[j] = lrow * pitch + (col < (uint32_t)N ? col * (uint32_t)sizeof(TO) : 0x80000000u);
+        }
+        asm volatile("" : "+v"(vo[0]), "+v"(vo[1]));  // not hoisted into the K loop
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    // row step of the block: < 128 rows, so < 2^31 with the column
+                    const int so = (int)((32 * i + 8 * (r >> 2) + (r & 3)) * pitch);
+                    float o = alpha * acc[i][j][r];
+                    if (beta != 0.0f) {
+                        const float c = __builtin_bit_cast(
+                            float, __builtin_amdgcn_raw_buffer_load_b32(rc, (int)vo[j], so, 0));
+                        const float cb = beta * c;
+                        o = o + cb;
+                    }
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, o), rc,
+                                                          (int)vo[j], so, 0);
+                }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -786,13 +824,14 @@ __device__ __forceinline__ void w8_epilogue(const phx_f16v (&acc)[4][2], TOut *C
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int64_t row = r0 + 32 * i + 8 * (r >> 2) + lrow + (r & 3);
-                TOut *dst = C + row * ldc + c0 + 32 * j + lcol;
+                const int64_t col = c0 + 32 * j + lcol;
+                TO *dst = C + row * ldc + col;
                 float o = alpha * acc[i][j][r];
                 if (beta != 0.0f) {
                     const float cb = beta * (float)*dst;
                     o = o + cb;
                 }
-                *dst = (TOut)o;
+                *dst = (TO)o;
             }
 }
 
@@ -829,7 +868,7 @@ struct Regs8 {
 // B chunk i = k row 16 i + t/32, n chunk t%32.  Each chunk is 8 f32 (two
 // 16-byte loads), rounded to one 16-byte f16 chunk in LDS.
 __device__ __forceinline__ void w8_load_a(Regs8 &R, __amdgpu_buffer_rsrc_t ra, uint32_t voa,
-                                          uint32_t lda, int i) {
+                                          uint32_t lda, int i) {  // voa: this step's lane offset
     R.a[i] = load_chunk(ra, voa, (int)((uint32_t)(i * 128 * lda) * ESZ));
 }
 __device__ __forceinline__ void w8_load_b(Regs8 &R, __amdgpu_buffer_rsrc_t rb, uint32_t vob,
@@ -865,20 +904,23 @@ __device__ __forceinline__ void w8_chunk(Regs8 &R, char *fill, __amdgpu_buffer_r
     }
 }
 
+template <bool RG>
 __device__ __forceinline__ void w8_step(phx_f16v (&acc)[4][2], Frags8 &F0, Frags8 &F1,
                                         const char *cur, const char *nxt, char *fill, Regs8 &R,
                                         const TIn *A, uint32_t lda, const TIn *B, uint32_t ldb,
-                                        uint32_t K, uint32_t m0, uint32_t n0, uint32_t kt,
-                                        uint32_t voa, uint32_t vob, uint32_t wm, uint32_t wn,
-                                        uint32_t tid, uint32_t lane) {
+                                        uint32_t M, uint32_t N, uint32_t K, uint32_t m0,
+                                        uint32_t n0, uint32_t kt, uint32_t voa, uint32_t voa_t,
+                                        uint32_t vob, uint32_t wm, uint32_t wn, uint32_t tid,
+                                        uint32_t lane) {
     const uint32_t kn = (kt + 3) * BK;  // the step whose data the reloads fetch
-    const __amdgpu_buffer_rsrc_t ra = a_rsrc<false>(A, lda, 0, K, m0, kn);
-    const __amdgpu_buffer_rsrc_t rb = b_rsrc<false>(B, ldb, 0, K, n0, kn);
+    const __amdgpu_buffer_rsrc_t ra = a_rsrc<RG>(A, lda, M, K, m0, kn);
+    const __amdgpu_buffer_rsrc_t rb = b_rsrc<RG>(B, ldb, N, K, n0, kn);
+    const uint32_t va = a_lane_off<RG>(voa, voa_t, K, kn);
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
         w8_mfma(acc, F0, m);
         if (m >= W8_RD && m < W8_RD + 6) w8_read(F1, cur, 1, wm, wn, lane, m - W8_RD);
-        if (m == W8_A0 || m == W8_A1) w8_chunk(R, fill, ra, rb, voa, vob, lda, ldb, tid, m == W8_A0 ? 0 : 1);
+        if (m == W8_A0 || m == W8_A1) w8_chunk(R, fill, ra, rb, va, vob, lda, ldb, tid, m == W8_A0 ? 0 : 1);
         __builtin_amdgcn_sched_barrier(0);
     }
     PHX_WAIT_VM_LGKM0(63);  // this wave's F1 reads and fill stores are done
@@ -888,42 +930,35 @@ __device__ __forceinline__ void w8_step(phx_f16v (&acc)[4][2], Frags8 &F0, Frags
     for (int m = 0; m < 8; ++m) {
         w8_mfma(acc, F1, m);
         if (m >= W8_RD && m < W8_RD + 6) w8_read(F0, nxt, 0, wm, wn, lane, m - W8_RD);
-        if (m == W8_B0 || m == W8_B1) w8_chunk(R, fill, ra, rb, voa, vob, lda, ldb, tid, m == W8_B0 ? 2 : 3);
+        if (m == W8_B0 || m == W8_B1) w8_chunk(R, fill, ra, rb, va, vob, lda, ldb, tid, m == W8_B0 ? 2 : 3);
         __builtin_amdgcn_sched_barrier(0);
     }
 }
 
-#define W8S(CUR, NXT, FILL, KT)                                                               \
-    w8_step(acc, F0, F1, CUR, NXT, FILL, R, A, lda, B, ldb, (uint32_t)K, m0, n0, KT, voa, vob, \
-            wm, wn, tid, lane)
-extern "C" __global__ __launch_bounds__(W8_NT, 1) void gemm_w8(PHX_MEMREF2(TIn, a, int64_t),
-                                                                PHX_MEMREF2(TIn, b, int64_t),
-                                                                PHX_MEMREF2(TOut, c, int64_t),
-                                                                float alpha, float beta) {
-    __shared__ __attribute__((aligned(16))) char stg[3 * STAGE_BYTES];
-    const int64_t M = a_s0, K = a_s1, N = b_s1;
-    if (blockDim.x != W8_NT || M % BM || N % BN || K % BK || M <= 0 || N <= 0 || K <= 0 ||
-        b_s0 != K || c_s0 != M || c_s1 != N || a_st1 != 1 || b_st1 != 1 || c_st1 != 1 ||
-        a_st0 % PHX_TC_K_MULT || (b_st0 | c_st0) % PHX_TC_N_MULT || M > INT32_MAX ||
-        (BM + 1) * (a_st0 > b_st0 ? a_st0 : b_st0) * (int64_t)sizeof(TIn) > INT32_MAX ||
-        ((uintptr_t)(a_ptr + a_off) | (uintptr_t)(b_ptr + b_off) | (uintptr_t)(c_ptr + c_off)) & 15)
-        return;
-    const TIn *A = a_ptr + a_off;
-    const TIn *B = b_ptr + b_off;
-    TOut *C = c_ptr + c_off;
-    const uint32_t lda = (uint32_t)a_st0, ldb = (uint32_t)b_st0;
-    const int64_t ldc = c_st0;
+// The eight-wave body over tiles t0, t0 + tstride, ... (as gemm_body).  RG:
+// M, N or K is not a whole number of tiles; the operand resources then end
+// at the matrix edges, A's chunks past K in the last step read zero, and
+// the epilogue skips rows and columns past the edges.
+#define W8S(CUR, NXT, FILL, KT)                                                              \
+    w8_step<RG>(acc, F0, F1, CUR, NXT, FILL, R, A, lda, B, ldb, (uint32_t)M, (uint32_t)N,     \
+                (uint32_t)K, m0, n0, KT, voa, voa_t, vob, wm, wn, tid, lane)
+template <bool RG, typename TO>
+__device__ __forceinline__ void w8_body(const TIn *A, const TIn *B, TO *C, uint32_t lda,
+                                        uint32_t ldb, int64_t ldc, int64_t M, int64_t N,
+                                        int64_t K, float alpha, float beta, uint32_t t0,
+                                        uint32_t tstride, char *stg) {
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t wm = (wave >> 2) * W8_WM, wn = (wave & 3) * W8_WN;
-    const uint32_t tiles_n = (uint32_t)(N / BN), tiles_m = (uint32_t)(M / BM);
-    const uint32_t ntiles = tiles_m * tiles_n, nblk = phx_block_count();
-    const uint32_t nk = (uint32_t)(K / BK);
+    const uint32_t tiles_n = (uint32_t)((N + BN - 1) / BN), tiles_m = (uint32_t)((M + BM - 1) / BM);
+    const uint32_t ntiles = tiles_m * tiles_n, nblk = tstride;
+    const uint32_t nk = (uint32_t)((K + BK - 1) / BK);
     const uint32_t voa = ((tid >> 2) * lda + (tid & 3) * 8) * ESZ;
+    const uint32_t voa_t = a_tail_off(voa, (tid & 3) * 8, (uint32_t)K);  // 8 k per chunk, K % 8 == 0
     const uint32_t vob = ((tid >> 5) * ldb + (tid & 31) * 8) * ESZ;
     char *const S0 = stg, *const S1 = stg + STAGE_BYTES, *const S2 = stg + 2 * STAGE_BYTES;
 
-    for (uint32_t t = phx_block_linear(); t < ntiles; t += nblk) {
+    for (uint32_t t = t0; t < ntiles; t += nblk) {
         const uint32_t ts = nblk == ntiles ? phx_xcd_swizzle(t, ntiles) : t;
         const uint32_t gsz = GROUP_M * tiles_n;
         const uint32_t g0 = (ts / gsz) * GROUP_M;
@@ -940,13 +975,14 @@ extern "C" __global__ __launch_bounds__(W8_NT, 1) void gemm_w8(PHX_MEMREF2(TIn, 
         Regs8 R;
         {   // prologue: steps 0 and 1 into stages 0 and 1, step 2 in flight in R
             for (int p = 0; p < 3; ++p) {
-                const __amdgpu_buffer_rsrc_t ra = a_rsrc<false>(A, lda, 0, (uint32_t)K, m0, p * BK);
-                const __amdgpu_buffer_rsrc_t rb = b_rsrc<false>(B, ldb, 0, (uint32_t)K, n0, p * BK);
+                const __amdgpu_buffer_rsrc_t ra = a_rsrc<RG>(A, lda, (uint32_t)M, (uint32_t)K, m0, p * BK);
+                const __amdgpu_buffer_rsrc_t rb = b_rsrc<RG>(B, ldb, (uint32_t)N, (uint32_t)K, n0, p * BK);
+                const uint32_t va = a_lane_off<RG>(voa, voa_t, (uint32_t)K, p * BK);
                 char *prev = stg + (p - 1) * STAGE_BYTES;  // step p-1's stage
 #pragma unroll
                 for (int i = 0; i < 2; ++i) {
                     if (p > 0) w8_store_a(R, prev, tid, i);
-                    w8_load_a(R, ra, voa, lda, i);
+                    w8_load_a(R, ra, va, lda, i);
                     if (p > 0) w8_store_b(R, prev, tid, i);
                     w8_load_b(R, rb, vob, ldb, i);
                 }
@@ -967,7 +1003,59 @@ extern "C" __global__ __launch_bounds__(W8_NT, 1) void gemm_w8(PHX_MEMREF2(TIn, 
         PHX_WAIT_VMCNT(0);  // the loads past K (zeros) before the stages are reused
         __syncthreads();
 
-        w8_epilogue(acc, C, ldc, m0 + wm, n0 + wn, alpha, beta, lane);
+        w8_epilogue<RG, TO>(acc, C, ldc, M, N, m0 + wm, n0 + wn, alpha, beta, lane);
     }
+}
+#undef W8S
+
+// The operand checks both eight-wave entries share with gemm (the host
+// refuses what fails them before launching).
+#define W8_SHAPE_OK(LDA, LDB, LDC, TO)                                                        \
+    (blockDim.x == W8_NT && N % PHX_TC_N_MULT == 0 && K % PHX_TC_K_MULT == 0 && M > 0 &&     \
+     N > 0 && K > 0 && (LDA) % PHX_TC_K_MULT == 0 && ((LDB) | (LDC)) % PHX_TC_N_MULT == 0 && \
+     M <= INT32_MAX && (BM + 1) * ((LDA) > (LDB) ? (LDA) : (LDB)) * (int64_t)sizeof(TIn) <= INT32_MAX && \
+     (BM + 1) * (LDC) * (int64_t)sizeof(TO) <= INT32_MAX)
+
+extern "C" __global__ __launch_bounds__(W8_NT, 1) void gemm_w8(PHX_MEMREF2(TIn, a, int64_t),
+                                                                PHX_MEMREF2(TIn, b, int64_t),
+                                                                PHX_MEMREF2(TOut, c, int64_t),
+                                                                float alpha, float beta) {
+    __shared__ __attribute__((aligned(16))) char stg[3 * STAGE_BYTES];
+    const int64_t M = a_s0, K = a_s1, N = b_s1;
+    if (!W8_SHAPE_OK(a_st0, b_st0, c_st0, TOut) || b_s0 != K || c_s0 != M || c_s1 != N ||
+        a_st1 != 1 || b_st1 != 1 || c_st1 != 1 ||
+        ((uintptr_t)(a_ptr + a_off) | (uintptr_t)(b_ptr + b_off) | (uintptr_t)(c_ptr + c_off)) & 15)
+        return;
+    const TIn *A = a_ptr + a_off;
+    const TIn *B = b_ptr + b_off;
+    TOut *C = c_ptr + c_off;
+    if (M % BM == 0 && N % BN == 0 && K % BK == 0)  // uniform
+        w8_body<false, TOut>(A, B, C, (uint32_t)a_st0, (uint32_t)b_st0, c_st0, M, N, K, alpha,
+                             beta, phx_block_linear(), phx_block_count(), stg);
+    else
+        w8_body<true, TOut>(A, B, C, (uint32_t)a_st0, (uint32_t)b_st0, c_st0, M, N, K, alpha,
+                            beta, phx_block_linear(), phx_block_count(), stg);
+}
+
+// Split-K on the eight-wave body: the same contract as gemm_splitk (raw f32
+// sums of K columns [y * kchunk, min(K, (y+1) * kchunk)) to W + y * M * N).
+extern "C" __global__ __launch_bounds__(W8_NT, 1) void gemm_w8_splitk(const TIn *A, const TIn *B,
+                                                                       float *W, int64_t lda,
+                                                                       int64_t ldb, int64_t M,
+                                                                       int64_t N, int64_t K,
+                                                                       int64_t kchunk) {
+    __shared__ __attribute__((aligned(16))) char stg[3 * STAGE_BYTES];
+    const int64_t k0 = (int64_t)blockIdx.y * kchunk;
+    if (!W8_SHAPE_OK(lda, ldb, N, float) || k0 >= K || kchunk % BK) return;
+    const int64_t kc = K - k0 < kchunk ? K - k0 : kchunk;
+    const TIn *As = A + k0;
+    const TIn *Bs = B + k0 * ldb;
+    float *Ws = W + (int64_t)blockIdx.y * M * N;
+    if (M % BM == 0 && N % BN == 0 && kc % BK == 0)
+        w8_body<false, float>(As, Bs, Ws, (uint32_t)lda, (uint32_t)ldb, N, M, N, kc, 1.0f, 0.0f,
+                              blockIdx.x, gridDim.x, stg);
+    else
+        w8_body<true, float>(As, Bs, Ws, (uint32_t)lda, (uint32_t)ldb, N, M, N, kc, 1.0f, 0.0f,
+                             blockIdx.x, gridDim.x, stg);
 }
 #endif

@@ -26,7 +26,7 @@
 #define PHX_H_BN 256
 #define PHX_H_BK 32
 #define PHX_H_THREADS 256
-#define PHX_TC_W8_THREADS 512  // gemm_w8: the whole-tile tc kernel, 8 waves
+#define PHX_TC_W8_THREADS 512  // gemm_w8, gemm_w8_splitk: the eight-wave tc kernels
 #define PHX_TC_N_MULT 4    // gemm_fp16tc_fp32acc (f32 storage): N % 4, K % 8
 #define PHX_TC_K_MULT 8
 #define PHX_H16_NK_MULT 8  // gemm_fp16 (f16 storage): N % 8, K % 8

@@ -486,8 +486,14 @@ int gemm_split(phx_kernel k, int64_t M, int64_t N, int64_t K) {
     return round_split(steps, sp);
 }
 
-// Whether a gemm_fp16tc_fp32acc launch runs the eight-wave kernel gemm_w8
-// (whole 256 x 256 tiles and 32-deep K steps).  gemm_fp16, whose operand
+// Whether a gemm_fp16tc_fp32acc launch runs the eight-wave kernels
+// (gemm_w8, and gemm_w8_splitk for a split) rather than the one-wave ones
+// (gemm, gemm_splitk): always, unless the plan pins variant 1.  Measured on
+// one box, three alternations: 4096^3 139-141 against 147-154 us, 4000^3
+// 134-140 against 146-154, 3000 x 5000 x 1000 49 against 51.5, split
+// 2048^3 (2 chunks) 41.5 against 47.0, 512^3 (2) 14.6 against 16.6, and
+// within 2% elsewhere (4088^3, 1000^3 and 640 x 768 x 4104 split 13 ways).
+// gemm_fp16, whose operand
 // copies are half the bytes and already overlap its MFMAs, measured the
 // same with an eight-wave form (114-119 vs 115-118 us) and keeps its
 // one-wave kernel.  PHX_GEMM_W8=0 in the environment turns it off, for
@@ -495,12 +501,8 @@ int gemm_split(phx_kernel k, int64_t M, int64_t N, int64_t K) {
 static bool gemm_w8(phx_kernel k, int64_t M, int64_t N, int64_t K) {
     if (k != PHX_GEMM_FP16TC_FP32ACC) return false;
     phx_plan pin;
-    if (const char *env = getenv("PHX_GEMM_W8")) {
-        if (atoi(env) == 0) return false;
-    } else if (pinned_plan(gemm_key(k, M, N, K), &pin) && pin.variant == 1) {
-        return false;
-    }
-    return M % PHX_H_BM == 0 && N % PHX_H_BN == 0 && K % PHX_H_BK == 0;
+    if (const char *env = getenv("PHX_GEMM_W8")) return atoi(env) != 0;
+    return !(pinned_plan(gemm_key(k, M, N, K), &pin) && pin.variant == 1);
 }
 
 // K columns per chunk of a split into sp chunks (a multiple of 32).
@@ -521,15 +523,17 @@ int launch_gemm_split_ws(phx_kernel k, const Desc *t, int64_t M, int64_t N, int6
                          float alpha, float beta, int sp, hipStream_t s, uint64_t ws) {
     const char *file = kSpecs[k].file;
     hipFunction_t fk, fr;
-    if (int rc = aux_function(file, "gemm_splitk", &fk)) return rc;
+    const bool w8 = gemm_w8(k, M, N, K);
+    if (int rc = aux_function(file, w8 ? "gemm_w8_splitk" : "gemm_splitk", &fk)) return rc;
     if (int rc = aux_function(file, "gemm_splitk_reduce", &fr)) return rc;
     const int64_t tiles = ((M + PHX_H_BM - 1) / PHX_H_BM) * ((N + PHX_H_BN - 1) / PHX_H_BN);
     uint64_t a = t[0].ptr, b = t[1].ptr, c = t[2].ptr;
     int64_t lda = t[0].stride[0], ldb = t[1].stride[0], ldc = t[2].stride[0];
     int64_t kchunk = split_chunk(K, sp);
     void *ka[] = {&a, &b, &ws, &lda, &ldb, &M, &N, &K, &kchunk};
-    hipError_t e = hipModuleLaunchKernel(fk, (uint32_t)tiles, (uint32_t)sp, 1, PHX_H_THREADS, 1, 1,
-                                         0, s, ka, nullptr);
+    hipError_t e = hipModuleLaunchKernel(fk, (uint32_t)tiles, (uint32_t)sp, 1,
+                                         w8 ? PHX_TC_W8_THREADS : PHX_H_THREADS, 1, 1, 0, s, ka,
+                                         nullptr);
     if (e != hipSuccess) return hip_error(e, "hipModuleLaunchKernel(gemm_splitk)");
     int32_t s32 = sp;
     void *ra[] = {&ws, &s32, &c, &ldc, &M, &N, &alpha, &beta};
@@ -670,7 +674,8 @@ int launch_raw(hipFunction_t f, const uint32_t grid[3], const uint32_t block[3],
             if (gemm_w8((phx_kernel)k, d[0], d[1], d[2])) {
                 hipFunction_t fw;
                 if (int rc = aux_function(kSpecs[k].file, "gemm_w8", &fw)) return rc;
-                const uint32_t tiles = (uint32_t)((d[0] / PHX_H_BM) * (d[1] / PHX_H_BN));
+                const uint32_t tiles = (uint32_t)(((d[0] + PHX_H_BM - 1) / PHX_H_BM) *
+                                                  ((d[1] + PHX_H_BN - 1) / PHX_H_BN));
                 hipError_t e = hipModuleLaunchKernel(fw, tiles, 1, 1, PHX_TC_W8_THREADS, 1, 1, 0,
                                                      s, args, nullptr);
                 if (e != hipSuccess) return hip_error(e, "hipModuleLaunchKernel(gemm_w8)");
@@ -1132,8 +1137,7 @@ int phx_plan_get(phx_kernel k, const int64_t *dims, int ndims, phx_plan *plan) {
     plan->variant = 0;
     if (is_gemm(k)) {
         plan->splits = gemm_split(k, dims[0], dims[1], dims[2]);
-        if (k == PHX_GEMM_FP16TC_FP32ACC && plan->splits == 1 &&
-            !gemm_w8(k, dims[0], dims[1], dims[2]))
+        if (k == PHX_GEMM_FP16TC_FP32ACC && !gemm_w8(k, dims[0], dims[1], dims[2]))
             plan->variant = 1;
         if (k == PHX_GEMM_FP32 && plan->splits == 1)
             plan->variant = s32_variant(dims[0], dims[1], dims[2]);

@@ -49,8 +49,8 @@ def _effective(units, sp):
 def gemm_space(kernel, M, N, K):
     """[(splits, variant)] for a GEMM: every distinct split count; for
     gemm_fp32 every other tiling (TILE_M x TILE_N x TILE_K, the @autotune
-    dims of examples/gemm_fp32.ph:1), unsplit; for gemm_fp16tc_fp32acc on
-    whole 256 x 256 tiles the one-wave kernel too."""
+    dims of examples/gemm_fp32.ph:1), unsplit; for gemm_fp16tc_fp32acc the
+    one-wave kernel, unsplit, too."""
     steps = -(-K // 32)
     space = []
     for sp in SPLITS:
@@ -59,7 +59,7 @@ def gemm_space(kernel, M, N, K):
             space.append((e, 0))
     if kernel == GEMM_FP32:
         space += [(1, v) for v in range(1, len(GEMM_FP32_TILINGS))]
-    if kernel == GEMM_FP16TC_FP32ACC and M % 256 == 0 and N % 256 == 0 and K % 32 == 0:
+    if kernel == GEMM_FP16TC_FP32ACC:
         space.append((1, 1))
     return space
 

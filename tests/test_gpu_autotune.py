@@ -105,8 +105,8 @@ def test_invalid_pins_are_refused(px_gpu):
 
 
 def test_tc_variant_pin_runs_the_one_wave_kernel(px_gpu, stream):
-    # variant 1 = the one-wave kernel on whole tiles; both kernels sum each
-    # output's K terms in the same order, so the outputs are bit-identical.
+    # variant 1 = the one-wave kernel; both kernels sum each output's K
+    # products in the same order, so the outputs are bit-identical.
     px = px_gpu
     kern, dims = px.GEMM_FP16TC_FP32ACC, [1024, 512, 2048]
     run, want = _gemm_case(px, stream, kern, *dims)

@@ -235,19 +235,24 @@ def test_bh_flash_split_matches_unsplit(px_gpu, stream, bits):
 
 
 @pytest.mark.parametrize("kern_name", ["GEMM_FP16TC_FP32ACC"])
-@pytest.mark.parametrize("M,N,K", [(512, 768, 2048), (1024, 256, 96), (256, 256, 32)])
-def test_eight_wave_kernel_matches_one_wave_kernel(px_gpu, stream, kern_name, M, N, K):
-    # Whole-tile gemm_fp16tc_fp32acc launches run gemm_w8 (two waves per
-    # SIMD); PHX_GEMM_W8=0 runs the one-wave kernel.  Both sum each output's
-    # K products in the same order, so they agree bit for bit, and both meet
-    # the oracle.
+@pytest.mark.parametrize("split", [1, 3])
+@pytest.mark.parametrize("M,N,K", [(512, 768, 2048), (1024, 256, 96), (256, 256, 32),
+                                   (300, 200, 104), (520, 388, 1000), (257, 260, 40),
+                                   (1000, 1000, 1000)])
+def test_eight_wave_kernel_matches_one_wave_kernel(px_gpu, stream, kern_name, M, N, K, split):
+    # gemm_fp16tc_fp32acc launches run the eight-wave kernels (gemm_w8, two
+    # waves per SIMD, and gemm_w8_splitk); PHX_GEMM_W8=0 runs the one-wave
+    # kernels.  Whole tiles and ragged edges (rows, columns and the last K
+    # step), unsplit and split in three: both sum each output's K products in
+    # the same order, so they agree bit for bit, and both meet the oracle.
+    # The guard past C catches stores beyond the last row.
     px = px_gpu
     kern = getattr(px, kern_name)
     A = oracle.f16_round(oracle.normal_f32(61, M * K, 1 / np.sqrt(K))).reshape(M, K)
     B = oracle.f16_round(oracle.normal_f32(62, K * N, 1 / np.sqrt(K))).reshape(K, N)
     C = oracle.normal_f32(63, M * N).reshape(M, N)
     outs = []
-    with _Env("PHX_GEMM_SPLIT", 1):
+    with _Env("PHX_GEMM_SPLIT", split):
         for w8 in (1, 0):
             with _Env("PHX_GEMM_W8", w8):
                 outs.append(_gemm(px, stream, kern, A, B, C, 0.75, -0.5))
