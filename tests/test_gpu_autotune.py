@@ -3,7 +3,7 @@
 
 The reference's autotuner (phobos-bench/src/autotune.rs:98-192) searches
 tile sizes; this backend searches the split count and, for
-gemm_fp16tc_fp32acc on whole tiles, which of its two kernels runs.  Every
+gemm_fp16tc_fp32acc, which of its two kernel families runs.  Every
 plan computes the same products and differs only in the order of the f32
 sums, so each is held to the same bounds as the unsplit launch: f32 GEMM
 1e-4 relative (floored at 1% of the RMS), f16 paths 2e-2 RMS-normalised,
