@@ -88,6 +88,10 @@ def parse():
                     help="pin the launch plan instead of searching it, as phobos-bench's "
                          "--autotune pins its tile dims (needs --bench): \"splits=N variant=V\", for "
                          "gemm_fp32 also \"TILE_M=128 TILE_N=128 TILE_K=16\"")
+    ap.add_argument("--pin", action="append", default=[], metavar="NAME=SPLITS,VARIANT",
+                    help="pin one benchmark's launch plan instead of searching it (repeatable), "
+                         "e.g. gemm_fp32=1,1: a profiling pass then runs the plans an earlier "
+                         "run's search picked")
     ap.add_argument("--no-autotune", action="store_true",
                     help="skip the launch-plan search and use the runtime's built-in plans")
     ap.add_argument("--shapes", action="store_true",
@@ -99,6 +103,14 @@ def parse():
         if args.bench not in BENCHES:
             ap.error(f"unknown --bench '{args.bench}'; available: {', '.join(BENCHES)}")
         args.kernels = args.bench
+    args.fixed = {}
+    for tok in args.pin:
+        name, eq, val = tok.partition("=")
+        parts = val.split(",")
+        if name not in BENCHES or name == "saxpy_fp32" or not eq or len(parts) != 2 or \
+                not all(p.strip().lstrip("-").isdigit() for p in parts):
+            ap.error(f"bad --pin '{tok}', expected NAME=SPLITS,VARIANT for a kernel with plans")
+        args.fixed[name] = (int(parts[0]), int(parts[1]))
     args.pins = {}
     if args.autotune is not None:
         # phobos-bench/src/main.rs:68-72, 118-119, 149-160: NAME=VALUE pins, one benchmark
@@ -312,12 +324,13 @@ def hbm_ceiling_leg(px, sets=4, nbytes=256 << 20, reps=3):
             "value": round(2 * nbytes * sets / (best / 1e3) / 1e9, 1), "unit": "GB/s"}
 
 
-def autotune_leg(px, stream, wanted, pins):
+def autotune_leg(px, stream, wanted, pins, fixed=None):
     """The launch-plan search of every benchmark kernel at its BASELINE
     shape and arguments, before the timed steps, as phobos-bench tunes each
     benchmark before it times it (main.rs:461-530); the winners stay pinned
     for the timed launches.  With pins (--autotune, one benchmark) the plan is
-    pinned without a search."""
+    pinned without a search, and so is a kernel's (splits, variant) in fixed
+    (--pin)."""
     from phobos_amd import autotune
     N = 4096
     jobs = {"gemm_fp32": ("gemm", px.GEMM_FP32, (N, N, N), dict(alpha=0.125, beta=1.5)),
@@ -331,6 +344,11 @@ def autotune_leg(px, stream, wanted, pins):
             continue  # saxpy has no plan choices
         kind, kid, dims, kw = jobs[name]
         pdims = list(dims) + ([64] if kind == "flash" else [])
+        if fixed and name in fixed:
+            px.plan_pin(kid, pdims, *fixed[name])
+            out[name] = {"pinned": list(px.plan_get(kid, pdims)),
+                         "plan": autotune.plan_name(kid, fixed[name])}
+            continue
         if pins:
             plan = autotune.plan_from_pins(kid, pins)
             px.plan_pin(kid, pdims, *plan)
@@ -580,7 +598,7 @@ def main():
     px.bind_workspace(stream, WORKSPACE_BYTES)
     tuned = None
     if not args.no_autotune and not args.hold:
-        tuned = autotune_leg(px, stream, wanted, args.pins)
+        tuned = autotune_leg(px, stream, wanted, args.pins, args.fixed)
     ks = setup(px, stream, wanted)
     if args.hold > 0:
         t0, n = time.perf_counter(), 0

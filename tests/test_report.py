@@ -67,5 +67,9 @@ def test_bench_cli_mirrors_phobos_bench_flags():
     assert r.returncode == 2 and "pass --bench to pick one" in r.stderr
     r = run("--bench", "gemm_fp16", "--autotune", "splits=two")
     assert r.returncode == 2 and "non-integer value 'two'" in r.stderr
+    for bad in ("gemm_fp32=1", "saxpy_fp32=1,0", "gemm_fp8=1,0", "flash_fp16=a,0"):
+        r = run("--pin", bad)  # --pin NAME=SPLITS,VARIANT, kernels with plans only
+        assert r.returncode == 2 and f"bad --pin '{bad}'" in r.stderr
     r = run("--help")
     assert r.returncode == 0 and "--bench NAME" in r.stdout and "--csv" in r.stdout
+    assert "--pin NAME=SPLITS,VARIANT" in r.stdout
