@@ -108,7 +108,7 @@ def parse():
         name, eq, val = tok.partition("=")
         parts = val.split(",")
         if name not in BENCHES or name == "saxpy_fp32" or not eq or len(parts) != 2 or \
-                not all(p.strip().lstrip("-").isdigit() for p in parts):
+                not all(p.strip().isdigit() for p in parts):
             ap.error(f"bad --pin '{tok}', expected NAME=SPLITS,VARIANT for a kernel with plans")
         args.fixed[name] = (int(parts[0]), int(parts[1]))
     args.pins = {}
@@ -345,7 +345,10 @@ def autotune_leg(px, stream, wanted, pins, fixed=None):
         kind, kid, dims, kw = jobs[name]
         pdims = list(dims) + ([64] if kind == "flash" else [])
         if fixed and name in fixed:
-            px.plan_pin(kid, pdims, *fixed[name])
+            try:
+                px.plan_pin(kid, pdims, *fixed[name])
+            except px.PhxError as e:  # a variant the kernel lacks, splits outside 1..16
+                sys.exit(f"bench.py: --pin {name}={fixed[name][0]},{fixed[name][1]}: {e}")
             out[name] = {"pinned": list(px.plan_get(kid, pdims)),
                          "plan": autotune.plan_name(kid, fixed[name])}
             continue
