@@ -14,8 +14,9 @@ the 256 MB MALL, which the next plan would then pay for).  The space here
 is the launch plan (phx_plan): the number of K chunks of a GEMM or key
 chunks of a flash launch, gemm_fp32's tile dims (TILE_M x TILE_N x TILE_K
 over the reference's ranges), and for gemm_fp16tc_fp32acc which of its
-two kernel families (eight-wave or one-wave) runs.  The winner is pinned with phx_plan_pin, so every
-later launch of that kernel at that shape uses it.
+two kernel families (eight-wave or one-wave) runs.  The winner is pinned
+with phx_plan_pin, so every later launch of that kernel at that shape uses
+it.
 
 A candidate is verified on its first launch against the unsplit plan's
 output (a split changes only the order of the f32 sums): relative to the
